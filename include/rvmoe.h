@@ -1,0 +1,158 @@
+/* rvmoe.h - MI355X (gfx950) quantized mixture-of-experts FFN path behind a C ABI.
+ *
+ * Conventions (same contract as the reference's runtime/hip/rvhip.h:1-14):
+ *   - every function returns 0 or a hipError_t code; no exception crosses the ABI;
+ *   - scalar arguments and null pointers are validated here (hipErrorInvalidValue);
+ *     buffer extents are the caller's contract;
+ *   - work is issued in order on the library's current stream (the null stream unless
+ *     rvm_set_stream selected another); rvh_download and rvh_sync synchronise;
+ *   - device pointers come from rvh_alloc and are released by rvh_free.
+ *
+ * Layouts:
+ *   Q4_0 row (reference/GGUF layout): k/32 blocks of {f16 d; u8 qs[16]}; value j =
+ *     ((qs[j] & 15) - 8) * d, value j + 16 = ((qs[j] >> 4) - 8) * d (rvhip.h:10-11).
+ *   Q8_0 row: k/32 blocks of {f16 d; i8 q[32]} (runtime/src/ops.rs:61-63, 94-105).
+ *   Packed Q4_0 (this library's HBM layout, produced by rvm_pack_q4 from Q4_0 rows): a
+ *     nibble plane followed by a scale plane, the same total size as the Q4_0 rows.
+ *     Rows are cut into tiles of 64 "lanes"; for tile t, step s and lane l the plane entry
+ *     index is (t * S + s) * 64 + l, holding 16 nibble bytes (qs XOR 0x88, so that every
+ *     nibble is the signed 4-bit weight) and one f16 scale.
+ *       RVM_PACK_GATE_UP: 64-row tiles; lane l < 32 is gate row 32t + l, lane l >= 32 is up
+ *         row n_out/2 + 32t + (l - 32); step s is block s (S = k/32).
+ *       RVM_PACK_ROWS32: 32-row tiles; lane l is row 32t + (l & 31) at block
+ *         (l >> 5) * S + s, with S = k/64.
+ *     Matrix m of a stack of n_mat matrices owns tiles m*T .. m*T + T-1.
+ *   Activations are row-major f32 [token][width].
+ */
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- Runtime, memory and events: same symbols and meaning as rvhip.h:22-38 ---- */
+int rvh_init(int device);
+int rvh_mem_info(size_t *free_bytes, size_t *total_bytes);
+int rvh_alloc(size_t bytes, void **out);
+int rvh_free(void *ptr);
+int rvh_upload(void *dst, const void *src, size_t bytes);
+int rvh_download(void *dst, const void *src, size_t bytes);
+int rvh_copy(void *dst, const void *src, size_t bytes); /* device to device, ordered */
+int rvh_sync(void);
+const char *rvh_error_string(int code);
+int rvh_event_create(void **out);
+int rvh_event_destroy(void *ev);
+int rvh_event_record(void *ev);
+int rvh_event_sync(void *ev);
+int rvh_event_elapsed(void *start, void *end, float *ms);
+
+/* ---- Reference expert-path kernels: same signatures and results as rvhip.h ---- */
+/* out[r] = ((x[r] * rms_scale) * post) * weight (weight may be NULL); rvhip.h:42-43. */
+int rvh_rms_norm(const float *x, float *out, const float *weight, int rows, int width, float eps, float post);
+/* y[t][r] = W[r] . x[t], f32 router GEMV; rvhip.h:49-50. */
+int rvh_f32_mm(const float *w, const float *x, float *y, int n_out, int k, int n_in);
+/* y[t][r] = W_q4[r] . x[t], Q4_0 rows (reference layout), f32 activations; rvhip.h:44-45. */
+int rvh_q4_mm(const void *w, const float *x, float *y, int n_out, int k, int n_in);
+/* Rows of 2*ff (gate then up) to rows of ff: gelu(gate) * up; rvhip.h:70-71. */
+int rvh_geglu_split(const float *gu, float *out, int rows, int ff);
+/* dst[i] = src[idx[i]], rows of width; rvhip.h:76-77. */
+int rvh_gather_rows(const float *src, const int32_t *idx, float *dst, int n, int width);
+/* out[t] = sum_j (y[pos[p]] * scale[p]) * weight[p], p = t*used + j, slot order; rvhip.h:78-80. */
+int rvh_moe_combine(const float *y, const int32_t *pos, const float *scale, const float *weight, float *out,
+                    int n_tok, int used, int width);
+
+/* ---- Additive MoE entry points (no counterpart symbol in rvhip.h) ---- */
+
+/* Select the stream for subsequent launches (NULL = null stream). The stream is a hipStream_t. */
+int rvm_set_stream(void *stream);
+int rvm_stream_create(void **out);
+int rvm_stream_destroy(void *stream);
+/* Capture the launches issued on the current (non-null) stream into a graph and instantiate it. */
+int rvm_graph_begin(void);
+int rvm_graph_end(void **graph_exec);
+int rvm_graph_launch(void *graph_exec);
+int rvm_graph_destroy(void *graph_exec);
+
+/* Packed Q4_0 formats (see the layout notes above). */
+#define RVM_PACK_GATE_UP 1
+#define RVM_PACK_ROWS32 2
+
+/* Bytes of n_mat packed matrices of n_out x k (equal to the Q4_0 row bytes). */
+int rvm_q4_packed_bytes(int n_mat, int n_out, int k, int format, size_t *bytes);
+/* Repack n_mat consecutive Q4_0 matrices (reference layout, n_out rows of k) on the device.
+ * Replaces the GGUF expert binding of runtime/src/model.rs:33-40 at load time. */
+int rvm_pack_q4(const void *src, void *dst, int n_mat, int n_out, int k, int format);
+
+/* Seeded synthetic Q4_0 matrices in the reference layout: scale f16(U(0.005, 0.02)), nibble
+ * bytes uniform; matrix m uses stream stream0 + m. The device and host variants write the
+ * same bytes. */
+int rvm_synth_q4(void *dst, int n_mat, int n_out, int k, uint64_t seed, uint64_t stream0);
+int rvm_synth_q4_host(void *dst, int n_mat, int n_out, int k, uint64_t seed, uint64_t stream0);
+
+/* Q8_0 activation quantisation of rows x k floats (k % 32 == 0): runtime/src/ops.rs:94-105. */
+int rvm_quantize_q8_0(const float *x, void *xq, int rows, int k);
+
+/* y[t][r] = W[r] . xq[t]: packed Q4_0 rows times Q8_0 activation rows, each block an exact int32
+ * sum scaled by d_w * d_x (runtime/src/expert_kernel.rs:85-95, 147-161). */
+int rvm_q4q8_mm(const void *w_packed, int format, const void *xq, float *y, int n_out, int k, int n_in);
+/* Per-block int32 sums of one activation row: sums[r][b] = sum_j w[r][32b+j] * q[32b+j]. */
+int rvm_q4q8_block_sums(const void *w_packed, int format, const void *xq, int32_t *sums, int n_out, int k);
+
+/* GeGLU then Q8_0: hq[r] = quantize_q8_0(gelu(gu[r][:ff]) * gu[r][ff:]) (runtime/src/exec.rs:606-611
+ * followed by runtime/src/expert_pool.rs:311-320). */
+int rvm_geglu_q8_0(const float *gu, void *hq, int rows, int ff);
+
+/* One MoE layer's device weights. */
+typedef struct rvm_layer {
+    int n_exp;                /* experts, <= 256 */
+    int top_k;                /* experts per token, <= 8 */
+    int d;                    /* model width, multiple of 256 */
+    int ff;                   /* expert width, multiple of 64 */
+    const float *router;      /* [n_exp][d] f32 row-major */
+    const float *router_bias; /* [n_exp] f32 added to the logits, or NULL */
+    const void *gate_up;      /* n_exp packed RVM_PACK_GATE_UP matrices of [2*ff][d] */
+    const void *down;         /* n_exp packed RVM_PACK_ROWS32 matrices of [d][ff] */
+    const float *down_scale;  /* [n_exp] f32 (down_exps_scale) or NULL for 1.0 */
+} rvm_layer;
+
+/* Flags for the layer entry points. */
+#define RVM_PRE_NORM 1     /* the layer input is rms_norm(x, eps) (runtime/src/ops.rs:131-139) */
+#define RVM_EXACT_SELECT 2 /* always recompute the router logits in the reference's order */
+
+/* Workspace bytes for n_tok tokens through rvm_moe_decode (n_tok = 1) or rvm_moe_forward.
+ * A workspace is zeroed once with rvm_workspace_init and may be reused by later calls on the
+ * same stream; concurrent calls need separate workspaces. */
+int rvm_moe_workspace_bytes(const rvm_layer *layer, int n_tok, size_t *bytes);
+int rvm_workspace_init(void *ws, size_t bytes);
+/* Router-selection exactness fallbacks taken in this workspace so far (synchronises). */
+int rvm_workspace_fallbacks(const void *ws, uint32_t *count);
+/* The expert ids and weights ([n_tok][top_k], top order) chosen by the last rvm_moe_decode /
+ * rvm_moe_forward call of n_tok tokens on this workspace, copied to host memory (synchronises);
+ * the reference's selection observer, runtime/src/exec.rs:519-526. */
+int rvm_workspace_selection(const rvm_layer *layer, int n_tok, const void *ws, int32_t *ids, float *weights);
+
+/* Router logits, softmax, top-k and renormalised weights for n_tok tokens (runtime/src/exec.rs:
+ * 493-517 with the plain projection W_r . x plus bias). ids[t][j] and weights[t][j] are in the
+ * reference's top order; logits (n_tok x n_exp, may be NULL) receives the f32 logits. */
+int rvm_router_select(const rvm_layer *layer, const float *x, int n_tok, int flags, float eps, int32_t *ids,
+                      float *weights, float *logits, void *ws, size_t ws_bytes);
+
+/* Stable grouping of n_pairs (token, slot) pairs by expert (runtime/src/exec.rs:540-558):
+ * order[k] = pair index sorted by (expert, pair); pos_of[pair] = k; group_start[e] .. group_start[e+1]
+ * is expert e's range of order (n_exp + 1 entries). */
+int rvm_moe_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of,
+                 int32_t *group_start);
+
+/* One decode token through one MoE layer: out[d] = sum_j down_j(geglu(gate_up_j(x))) * scale * weight,
+ * in slot order (runtime/src/exec.rs:456-475, 572-640; runtime/src/hip_exec.rs:780-843). */
+int rvm_moe_decode(const rvm_layer *layer, const float *x, float *out, int flags, float eps, void *ws,
+                   size_t ws_bytes);
+
+/* n_tok tokens through one MoE layer with device grouping (ragged decode batches and prefill). */
+int rvm_moe_forward(const rvm_layer *layer, const float *x, float *out, int n_tok, int flags, float eps, void *ws,
+                    size_t ws_bytes);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,214 @@
+// internal.hpp - shared device helpers for the gfx950 MoE kernels.
+//
+// Arithmetic notes (reference paths relative to the reference root):
+//  - Q4_0 x Q8_0 block dot (runtime/src/expert_kernel.rs:147-161): the packed nibble plane holds
+//    qs XOR 0x88, so every nibble is the signed weight w = n - 8. An activation q (int8) is split
+//    as q = 16*hi + lo' + 8 with hi = q >> 4 (the high nibble of the byte, signed) and
+//    lo' = (q & 15) - 8 (the low nibble XOR 8, signed). Then
+//        sum_j w_j q_j = 16 * sdot8(w, HI) + sdot8(w, LO) + 8 * sdot8(w, 0x11111111)
+//    with three v_dot8_i32_i4 chains of four dwords: an exact int32 for every block.
+//  - The f32 part is fma((float)sumi, d_w * d_x, acc) per block: the same per-block product as
+//    the reference; only the f32 accumulation order differs (tolerance class).
+//  - Everything is compiled with -ffp-contract=off; fmaf is written where a fused op is meant.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/rvmoe.h"
+
+namespace rvm {
+
+constexpr int QK = 32;
+constexpr int Q4_BLOCK = 18;
+constexpr int Q8_BLOCK = 34;
+// A prepared activation block: HI[4], LO[4] nibble dwords in the weight-nibble order, then d_x
+// (the f16-rounded scale as f32) and one spare dword: 40 bytes.
+constexpr int ACT_DW = 10;
+constexpr uint32_t ONES4 = 0x11111111u;
+constexpr int MAX_TOKENS = 65535;  // tokens per call (the router grid's y dimension)
+
+// Library state (runtime.hip).
+hipStream_t cur_stream();
+inline int launched() { return (int)hipGetLastError(); }
+inline int grid_blocks(size_t n, int per) { return (int)((n + per - 1) / per); }
+
+#define RVM_CHECK(cond)                                  \
+    do {                                                 \
+        if (!(cond)) return (int)hipErrorInvalidValue;   \
+    } while (0)
+#define RVM_TRY(expr)                      \
+    do {                                   \
+        hipError_t e_ = (expr);            \
+        if (e_ != hipSuccess) return (int)e_; \
+    } while (0)
+
+// IEEE binary16 bits -> f32, exact (same values as runtime/src/ops.rs:7-24).
+__device__ __forceinline__ float h2f(uint16_t u) {
+    _Float16 h;
+    __builtin_memcpy(&h, &u, 2);
+    return (float)h;
+}
+
+// f32 -> binary16 bits, round to nearest even, written out in integers so that the result is
+// the reference's f32_to_f16 (runtime/src/ops.rs:27-59) bit for bit, NaN payload included.
+__host__ __device__ __forceinline__ uint16_t f2h_rne(float f) {
+    uint32_t x = __builtin_bit_cast(uint32_t, f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    int32_t exp = (int32_t)((x >> 23) & 0xff);
+    uint32_t man = x & 0x7fffffu;
+    if (exp == 0xff) return (uint16_t)(sign | 0x7c00u | (man != 0 ? 0x200u : 0u));
+    int32_t e = exp - 127 + 15;
+    if (e >= 0x1f) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        uint32_t m = man | 0x800000u;
+        uint32_t shift = (uint32_t)(14 - e);
+        uint32_t half = 1u << (shift - 1);
+        uint32_t rem = m & ((1u << shift) - 1);
+        uint32_t r = m >> shift;
+        if (rem > half || (rem == half && (r & 1u))) r += 1;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = ((uint32_t)e << 10) | (man >> 13);
+    uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r += 1;
+    return (uint16_t)(sign | r);
+}
+
+// Rust `f32 as i8`: saturate, NaN to 0.
+__device__ __forceinline__ int sat_i8(float v) {
+    if (v != v) return 0;
+    if (v >= 127.0f) return 127;
+    if (v <= -128.0f) return -128;
+    return (int)v;
+}
+
+// tanh GELU in the reference's operation order (runtime/src/ops.rs:145-149).
+__device__ __forceinline__ float gelu(float x) {
+    const float A = 0.044715f;
+    const float S = 0.7978846f;
+    float inner = S * x * (1.0f + A * x * x);
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+// Exact int32 sum of one 32-element block: w4 = this lane's 16 packed nibble bytes, a = HI[4], LO[4].
+__device__ __forceinline__ int block_dot(uint4 w4, const uint32_t *a) {
+    int hi = __builtin_amdgcn_sdot8((int)w4.x, (int)a[0], 0, false);
+    hi = __builtin_amdgcn_sdot8((int)w4.y, (int)a[1], hi, false);
+    hi = __builtin_amdgcn_sdot8((int)w4.z, (int)a[2], hi, false);
+    hi = __builtin_amdgcn_sdot8((int)w4.w, (int)a[3], hi, false);
+    int lo = __builtin_amdgcn_sdot8((int)w4.x, (int)a[4], 0, false);
+    lo = __builtin_amdgcn_sdot8((int)w4.y, (int)a[5], lo, false);
+    lo = __builtin_amdgcn_sdot8((int)w4.z, (int)a[6], lo, false);
+    lo = __builtin_amdgcn_sdot8((int)w4.w, (int)a[7], lo, false);
+    int s1 = __builtin_amdgcn_sdot8((int)w4.x, (int)ONES4, 0, false);
+    s1 = __builtin_amdgcn_sdot8((int)w4.y, (int)ONES4, s1, false);
+    s1 = __builtin_amdgcn_sdot8((int)w4.z, (int)ONES4, s1, false);
+    s1 = __builtin_amdgcn_sdot8((int)w4.w, (int)ONES4, s1, false);
+    return (hi << 4) + lo + (s1 << 3);
+}
+
+// Prepared activation dwords from a raw Q8_0 block's 32 quant bytes, given as 8 dwords q[0..7]
+// (q[i] holds elements 4i..4i+3). Weight dword d pairs elements 4d..4d+3 (low nibbles) with
+// 16+4d..16+4d+3 (high nibbles).
+__device__ __forceinline__ void prep_from_q8(const uint32_t *q, uint32_t *a) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        uint32_t lo = q[d], hi = q[4 + d];
+        a[d] = ((lo >> 4) & 0x0f0f0f0fu) | (hi & 0xf0f0f0f0u);
+        a[4 + d] = ((lo & 0x0f0f0f0fu) | ((hi & 0x0f0f0f0fu) << 4)) ^ 0x88888888u;
+    }
+}
+
+// Q8_0 quantisation of one 32-value block held by a 32-lane half-wave (lane j of the half
+// holds element j), as runtime/src/ops.rs:95-105: amax fold from 0 ignoring NaN, d = amax/127,
+// id = 1/d (0 when d == 0), q = round-half-away(v * id) saturated. Returns q for this lane and
+// the f16 bits of d in *dbits (same in every lane of the half).
+__device__ __forceinline__ int quant_q8_half(float v, uint16_t *dbits) {
+    float m = fmaxf(0.0f, fabsf(v));
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    float d = m / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    *dbits = f2h_rne(d);
+    return sat_i8(roundf(v * id));
+}
+
+// Build the prepared block from the 32 quants of a half-wave (lane j of the half holds q_j) and
+// store it at dst (ACT_DW dwords) when ok. Element 4d+k (k < 4) sits in byte k, low nibble, of
+// dword d; element 16+4d+k in byte k, high nibble. Every lane of the wave must call this.
+__device__ __forceinline__ void store_prep_half(int q, uint16_t dbits, int j, uint32_t *dst, bool ok) {
+    const int k = j & 3;
+    const int sh = 8 * k + (j >= 16 ? 4 : 0);
+    uint32_t ch = (uint32_t)((q >> 4) & 15) << sh;
+    uint32_t cl = (uint32_t)((q & 15) ^ 8) << sh;
+    ch |= __shfl_xor(ch, 1);
+    cl |= __shfl_xor(cl, 1);
+    ch |= __shfl_xor(ch, 2);
+    cl |= __shfl_xor(cl, 2);
+    ch |= __shfl_xor(ch, 16);
+    cl |= __shfl_xor(cl, 16);
+    if (!ok) return;
+    if (j < 16 && k == 0) dst[j >> 2] = ch;
+    if (j < 16 && k == 1) dst[4 + (j >> 2)] = cl;
+    if (j == 16) dst[8] = __builtin_bit_cast(uint32_t, h2f(dbits));
+    if (j == 17) dst[9] = 0u;
+}
+
+// Workspace layout for n_tok tokens through one layer (offsets in bytes, 256-aligned).
+struct WsLayout {
+    size_t ctl;     // u32[64]: [0] router-guard fallback count
+    size_t tokctr;  // u32[MAX_TOKENS] last-block-done counters of the router kernel, at a fixed
+                    // place for every n_tok so that calls of different sizes share zeroed counters
+    size_t stats;   // double2[n_tok][n_exp]: exact-sum estimate and error bound per logit
+    size_t ids;     // i32[n_tok][top_k]
+    size_t wts;     // f32[n_tok][top_k]
+    size_t xact;    // u32[n_tok][d/32][ACT_DW]
+    size_t hact;    // u32[pairs][ff/32][ACT_DW]
+    size_t order;   // i32[pairs]
+    size_t pos_of;  // i32[pairs]
+    size_t gstart;  // i32[n_exp + 1]
+    size_t y;       // f32[pairs][d]
+    size_t total;
+};
+
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+inline WsLayout ws_layout(const rvm_layer *L, int n_tok) {
+    WsLayout w{};
+    size_t o = 0;
+    size_t pairs = (size_t)n_tok * L->top_k;
+    auto take = [&](size_t bytes) {
+        size_t at = o;
+        o = align256(o + bytes);
+        return at;
+    };
+    w.ctl = take(256);
+    w.tokctr = take((size_t)MAX_TOKENS * 4);
+    w.stats = take((size_t)n_tok * L->n_exp * 16);
+    w.ids = take(pairs * 4);
+    w.wts = take(pairs * 4);
+    w.xact = take((size_t)n_tok * (L->d / QK) * ACT_DW * 4);
+    w.hact = take(pairs * (L->ff / QK) * ACT_DW * 4);
+    w.order = take(pairs * 4);
+    w.pos_of = take(pairs * 4);
+    w.gstart = take((size_t)(L->n_exp + 1) * 4);
+    w.y = n_tok > 1 ? take(pairs * L->d * 4) : take(0);
+    w.total = o;
+    return w;
+}
+
+// Layer validation shared by the layer entry points.
+inline bool layer_ok(const rvm_layer *L) {
+    return L && L->router && L->gate_up && L->down && L->n_exp > 0 && L->n_exp <= 256 && L->top_k > 0 &&
+           L->top_k <= 8 && L->top_k <= L->n_exp && L->d > 0 && L->d % 256 == 0 && L->d <= 16384 && L->ff > 0 &&
+           L->ff % 64 == 0 && L->ff <= 4096;
+}
+
+// Kernel launchers shared across translation units.
+int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, float eps, uint8_t *ws,
+                  const WsLayout &lay, int32_t *ids, float *wts, float *logits);
+int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart);
+
+}  // namespace rvm

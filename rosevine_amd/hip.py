@@ -1,0 +1,342 @@
+"""Safe host view of the C ABI in include/rvmoe.h (librvmoe.so).
+
+Mirrors the reference's Rust wrapper runtime/src/hip.rs: device memory is owned by `DevBuf`
+and freed when it is closed or collected (hip.rs:240-310); every wrapper checks the byte range a
+kernel reads or writes against the owning allocation before calling it, because the C side
+validates only scalars (hip.rs:1-6, 258-263, 362-586); a non-zero return code becomes
+`DeviceError(code)` (hip.rs:120-122, error.rs `Error::Device`).
+
+There is no CPU fallback: if the HIP library is missing the import of this module's `lib()`
+raises, naming the build step.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librvmoe.so")
+
+QK, Q4_BLOCK, Q8_BLOCK = 32, 18, 34
+PACK_GATE_UP, PACK_ROWS32 = 1, 2
+PRE_NORM, EXACT_SELECT = 1, 2
+
+
+class DeviceError(RuntimeError):
+    """A HIP error code returned through the ABI."""
+
+    def __init__(self, code: int):
+        self.code = code
+        msg = lib().rvh_error_string(code)
+        super().__init__(f"device error {code}: {msg.decode() if msg else '?'}")
+
+
+class BoundsError(ValueError):
+    """A kernel's byte range does not fit its buffer (refused before any launch)."""
+
+
+class RvmLayer(C.Structure):
+    """`rvm_layer` of include/rvmoe.h."""
+
+    _fields_ = [
+        ("n_exp", C.c_int),
+        ("top_k", C.c_int),
+        ("d", C.c_int),
+        ("ff", C.c_int),
+        ("router", C.c_void_p),
+        ("router_bias", C.c_void_p),
+        ("gate_up", C.c_void_p),
+        ("down", C.c_void_p),
+        ("down_scale", C.c_void_p),
+    ]
+
+
+_lib = None
+
+# name -> (restype, argtypes); every symbol of include/rvmoe.h.
+_vp, _sz, _i, _f, _u64 = C.c_void_p, C.c_size_t, C.c_int, C.c_float, C.c_uint64
+_PL = C.POINTER(RvmLayer)
+SIGNATURES = {
+    "rvh_init": (_i, [_i]),
+    "rvh_mem_info": (_i, [C.POINTER(_sz), C.POINTER(_sz)]),
+    "rvh_alloc": (_i, [_sz, C.POINTER(_vp)]),
+    "rvh_free": (_i, [_vp]),
+    "rvh_upload": (_i, [_vp, _vp, _sz]),
+    "rvh_download": (_i, [_vp, _vp, _sz]),
+    "rvh_copy": (_i, [_vp, _vp, _sz]),
+    "rvh_sync": (_i, []),
+    "rvh_error_string": (C.c_char_p, [_i]),
+    "rvh_event_create": (_i, [C.POINTER(_vp)]),
+    "rvh_event_destroy": (_i, [_vp]),
+    "rvh_event_record": (_i, [_vp]),
+    "rvh_event_sync": (_i, [_vp]),
+    "rvh_event_elapsed": (_i, [_vp, _vp, C.POINTER(_f)]),
+    "rvh_rms_norm": (_i, [_vp, _vp, _vp, _i, _i, _f, _f]),
+    "rvh_f32_mm": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "rvh_q4_mm": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "rvh_geglu_split": (_i, [_vp, _vp, _i, _i]),
+    "rvh_gather_rows": (_i, [_vp, _vp, _vp, _i, _i]),
+    "rvh_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
+    "rvm_set_stream": (_i, [_vp]),
+    "rvm_stream_create": (_i, [C.POINTER(_vp)]),
+    "rvm_stream_destroy": (_i, [_vp]),
+    "rvm_graph_begin": (_i, []),
+    "rvm_graph_end": (_i, [C.POINTER(_vp)]),
+    "rvm_graph_launch": (_i, [_vp]),
+    "rvm_graph_destroy": (_i, [_vp]),
+    "rvm_q4_packed_bytes": (_i, [_i, _i, _i, _i, C.POINTER(_sz)]),
+    "rvm_pack_q4": (_i, [_vp, _vp, _i, _i, _i, _i]),
+    "rvm_synth_q4": (_i, [_vp, _i, _i, _i, _u64, _u64]),
+    "rvm_synth_q4_host": (_i, [_vp, _i, _i, _i, _u64, _u64]),
+    "rvm_quantize_q8_0": (_i, [_vp, _vp, _i, _i]),
+    "rvm_q4q8_mm": (_i, [_vp, _i, _vp, _vp, _i, _i, _i]),
+    "rvm_q4q8_block_sums": (_i, [_vp, _i, _vp, _vp, _i, _i]),
+    "rvm_geglu_q8_0": (_i, [_vp, _vp, _i, _i]),
+    "rvm_moe_workspace_bytes": (_i, [_PL, _i, C.POINTER(_sz)]),
+    "rvm_workspace_init": (_i, [_vp, _sz]),
+    "rvm_workspace_fallbacks": (_i, [_vp, C.POINTER(C.c_uint32)]),
+    "rvm_workspace_selection": (_i, [_PL, _i, _vp, _vp, _vp]),
+    "rvm_router_select": (_i, [_PL, _vp, _i, _i, _f, _vp, _vp, _vp, _vp, _sz]),
+    "rvm_moe_plan": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
+    "rvm_moe_decode": (_i, [_PL, _vp, _vp, _i, _f, _vp, _sz]),
+    "rvm_moe_forward": (_i, [_PL, _vp, _vp, _i, _i, _f, _vp, _sz]),
+}
+
+
+def lib() -> C.CDLL:
+    """The HIP library. Raises if it has not been built (there is no CPU fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with `python -m rosevine_amd.build` "
+                              "(or __graft_entry__.build()); the MoE path has no CPU fallback")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(code: int) -> None:
+    if code != 0:
+        raise DeviceError(code)
+
+
+def init(device: int = 0) -> None:
+    check(lib().rvh_init(device))
+
+
+def sync() -> None:
+    check(lib().rvh_sync())
+
+
+def mem_info() -> tuple[int, int]:
+    free, total = C.c_size_t(), C.c_size_t()
+    check(lib().rvh_mem_info(C.byref(free), C.byref(total)))
+    return free.value, total.value
+
+
+class DevBuf:
+    """An owned device allocation (hip.rs `DevBuf`)."""
+
+    def __init__(self, nbytes: int):
+        if nbytes < 0:
+            raise BoundsError("negative size")
+        p = C.c_void_p()
+        check(lib().rvh_alloc(nbytes, C.byref(p)))
+        self.ptr = p.value
+        self.nbytes = nbytes
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DevBuf":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def close(self) -> None:
+        if getattr(self, "ptr", None):
+            lib().rvh_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def at(self, offset: int = 0, length: int = 0) -> int:
+        """Device address of [offset, offset + length), checked against the allocation."""
+        if not self.ptr:
+            raise BoundsError("buffer is closed")
+        if offset < 0 or length < 0 or offset + length > self.nbytes:
+            raise BoundsError(f"range [{offset}, {offset + length}) outside a {self.nbytes}-byte buffer")
+        return self.ptr + offset
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        check(lib().rvh_upload(self.at(offset, a.nbytes), a.ctypes.data, a.nbytes))
+
+    def download(self, dtype, count: int, offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype)
+        check(lib().rvh_download(out.ctypes.data, self.at(offset, out.nbytes), out.nbytes))
+        return out
+
+
+def _need(buf: DevBuf, nbytes: int, offset: int = 0) -> int:
+    return buf.at(offset, nbytes)
+
+
+class Event:
+    def __init__(self):
+        p = C.c_void_p()
+        check(lib().rvh_event_create(C.byref(p)))
+        self.ptr = p.value
+
+    def record(self) -> None:
+        check(lib().rvh_event_record(self.ptr))
+
+    def synchronize(self) -> None:
+        check(lib().rvh_event_sync(self.ptr))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        check(lib().rvh_event_elapsed(self.ptr, end.ptr, C.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                lib().rvh_event_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+class Stream:
+    """A non-blocking stream at the default priority; `use()` routes later launches to it."""
+
+    def __init__(self):
+        p = C.c_void_p()
+        check(lib().rvm_stream_create(C.byref(p)))
+        self.ptr = p.value
+
+    def use(self) -> None:
+        check(lib().rvm_set_stream(self.ptr))
+
+    @staticmethod
+    def use_default() -> None:
+        check(lib().rvm_set_stream(None))
+
+    def close(self) -> None:
+        if self.ptr:
+            lib().rvm_stream_destroy(self.ptr)
+            self.ptr = None
+
+
+class Graph:
+    """Launches captured on the current stream, instantiated once and replayed."""
+
+    def __init__(self, ptr: int):
+        self.ptr = ptr
+
+    @staticmethod
+    def begin() -> None:
+        check(lib().rvm_graph_begin())
+
+    @classmethod
+    def end(cls) -> "Graph":
+        p = C.c_void_p()
+        check(lib().rvm_graph_end(C.byref(p)))
+        return cls(p.value)
+
+    def launch(self) -> None:
+        check(lib().rvm_graph_launch(self.ptr))
+
+    def close(self) -> None:
+        if self.ptr:
+            lib().rvm_graph_destroy(self.ptr)
+            self.ptr = None
+
+
+# ---- kernel wrappers: ranges checked here, scalars in C ----
+
+def q4_packed_bytes(n_mat: int, n_out: int, k: int, fmt: int) -> int:
+    n = C.c_size_t()
+    check(lib().rvm_q4_packed_bytes(n_mat, n_out, k, fmt, C.byref(n)))
+    return n.value
+
+
+def pack_q4(src: DevBuf, dst: DevBuf, n_mat: int, n_out: int, k: int, fmt: int) -> None:
+    nbytes = q4_packed_bytes(n_mat, n_out, k, fmt)
+    check(lib().rvm_pack_q4(_need(src, nbytes), _need(dst, nbytes), n_mat, n_out, k, fmt))
+
+
+def synth_q4(dst: DevBuf, n_mat: int, n_out: int, k: int, seed: int, stream0: int) -> None:
+    nbytes = n_mat * n_out * (k // QK) * Q4_BLOCK
+    check(lib().rvm_synth_q4(_need(dst, nbytes), n_mat, n_out, k, seed, stream0))
+
+
+def synth_q4_host(n_mat: int, n_out: int, k: int, seed: int, stream0: int) -> np.ndarray:
+    out = np.empty(n_mat * n_out * (k // QK) * Q4_BLOCK, np.uint8)
+    check(lib().rvm_synth_q4_host(out.ctypes.data, n_mat, n_out, k, seed, stream0))
+    return out
+
+
+def quantize_q8_0(x: DevBuf, xq: DevBuf, rows: int, k: int) -> None:
+    check(lib().rvm_quantize_q8_0(_need(x, rows * k * 4), _need(xq, rows * (k // QK) * Q8_BLOCK), rows, k))
+
+
+def q4q8_mm(w: DevBuf, fmt: int, xq: DevBuf, y: DevBuf, n_out: int, k: int, n_in: int) -> None:
+    wb = q4_packed_bytes(1, n_out, k, fmt)
+    check(lib().rvm_q4q8_mm(_need(w, wb), fmt, _need(xq, n_in * (k // QK) * Q8_BLOCK), _need(y, n_in * n_out * 4),
+                            n_out, k, n_in))
+
+
+def q4q8_block_sums(w: DevBuf, fmt: int, xq: DevBuf, sums: DevBuf, n_out: int, k: int) -> None:
+    wb = q4_packed_bytes(1, n_out, k, fmt)
+    check(lib().rvm_q4q8_block_sums(_need(w, wb), fmt, _need(xq, (k // QK) * Q8_BLOCK),
+                                    _need(sums, n_out * (k // QK) * 4), n_out, k))
+
+
+def geglu_q8_0(gu: DevBuf, hq: DevBuf, rows: int, ff: int) -> None:
+    check(lib().rvm_geglu_q8_0(_need(gu, rows * 2 * ff * 4), _need(hq, rows * (ff // QK) * Q8_BLOCK), rows, ff))
+
+
+def rms_norm(x: DevBuf, out: DevBuf, weight: DevBuf | None, rows: int, width: int, eps: float, post: float) -> None:
+    w = None if weight is None else _need(weight, width * 4)
+    check(lib().rvh_rms_norm(_need(x, rows * width * 4), _need(out, rows * width * 4), w, rows, width, eps, post))
+
+
+def f32_mm(w: DevBuf, x: DevBuf, y: DevBuf, n_out: int, k: int, n_in: int) -> None:
+    check(lib().rvh_f32_mm(_need(w, n_out * k * 4), _need(x, n_in * k * 4), _need(y, n_in * n_out * 4), n_out, k,
+                           n_in))
+
+
+def q4_mm(w: DevBuf, x: DevBuf, y: DevBuf, n_out: int, k: int, n_in: int) -> None:
+    check(lib().rvh_q4_mm(_need(w, n_out * (k // QK) * Q4_BLOCK), _need(x, n_in * k * 4),
+                          _need(y, n_in * n_out * 4), n_out, k, n_in))
+
+
+def geglu_split(gu: DevBuf, out: DevBuf, rows: int, ff: int) -> None:
+    check(lib().rvh_geglu_split(_need(gu, rows * 2 * ff * 4), _need(out, rows * ff * 4), rows, ff))
+
+
+def gather_rows(src: DevBuf, src_rows: int, idx: DevBuf, dst: DevBuf, n: int, width: int) -> None:
+    check(lib().rvh_gather_rows(_need(src, src_rows * width * 4), _need(idx, n * 4), _need(dst, n * width * 4), n,
+                                width))
+
+
+def moe_combine(y: DevBuf, y_rows: int, pos: DevBuf, scale: DevBuf, weight: DevBuf, out: DevBuf, n_tok: int,
+                used: int, width: int) -> None:
+    pairs = n_tok * used
+    check(lib().rvh_moe_combine(_need(y, y_rows * width * 4), _need(pos, pairs * 4), _need(scale, pairs * 4),
+                                _need(weight, pairs * 4), _need(out, n_tok * width * 4), n_tok, used, width))
+
+
+def moe_plan(ids: DevBuf, n_pairs: int, n_exp: int, order: DevBuf, pos_of: DevBuf, group_start: DevBuf) -> None:
+    check(lib().rvm_moe_plan(_need(ids, n_pairs * 4), n_pairs, n_exp, _need(order, n_pairs * 4),
+                             _need(pos_of, n_pairs * 4), _need(group_start, (n_exp + 1) * 4)))

@@ -1,0 +1,231 @@
+"""Per-stage parity of the HIP kernels against the CPU oracle (GPU).
+
+The stages follow the reference's conformance tests (runtime/tests/hip_ops.rs:56-81, 402-443) and
+the build's rules: Q8_0 bytes and per-block int32 Q4xQ8 sums are bit-exact when both sides see
+the same inputs; f32 results agree within 1e-3 of the reference output's RMS (and within the
+reference's own per-row summation bound 4e-6 * sum|w x| * d, expert_kernel.rs:346-348).
+"""
+import numpy as np
+import pytest
+
+from rosevine_amd import hip
+from rosevine_amd.hip import DevBuf
+
+pytestmark = pytest.mark.gpu
+
+QK, Q4B, Q8B = 32, 18, 34
+
+
+def dev(a):
+    return DevBuf.from_array(np.ascontiguousarray(a))
+
+
+def rms(a):
+    return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
+
+
+def pack_np(rows, n_out, k, fmt):
+    """numpy statement of the packed layout in include/rvmoe.h (index arithmetic only)."""
+    nb = k // QK
+    blk = rows.reshape(n_out, nb, Q4B)
+    if fmt == hip.PACK_GATE_UP:
+        T, S = n_out // 64, nb
+        t, s, l = np.meshgrid(np.arange(T), np.arange(S), np.arange(64), indexing="ij")
+        row = np.where(l < 32, 32 * t + l, n_out // 2 + 32 * t + (l - 32))
+        b = s
+    else:
+        T, S = n_out // 32, nb // 2
+        t, s, l = np.meshgrid(np.arange(T), np.arange(S), np.arange(64), indexing="ij")
+        row = 32 * t + (l & 31)
+        b = (l >> 5) * S + s
+    sel = blk[row, b]  # [T, S, 64, 18]
+    nib = (sel[..., 2:] ^ 0x88).reshape(-1)
+    scl = sel[..., :2].reshape(-1)
+    return np.concatenate([nib, scl])
+
+
+def rand_q4(rng, n_out, k, lo=0.005, hi=0.02):
+    nb = k // QK
+    out = np.empty((n_out, nb, Q4B), np.uint8)
+    d = rng.uniform(lo, hi, (n_out, nb)).astype(np.float16)
+    out[:, :, :2] = d.reshape(n_out, nb, 1).view(np.uint8).reshape(n_out, nb, 2)
+    out[:, :, 2:] = rng.integers(0, 256, (n_out, nb, 16), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+def packed(rows, n_out, k, fmt):
+    src = dev(rows)
+    dst = DevBuf(rows.nbytes)
+    hip.pack_q4(src, dst, 1, n_out, k, fmt)
+    return dst
+
+
+def test_synth_device_matches_host(gpu):
+    for n_mat, n_out, k in [(2, 64, 256), (1, 1408, 2816), (3, 2816, 704)]:
+        n = n_mat * n_out * (k // QK) * Q4B
+        buf = DevBuf(n)
+        hip.synth_q4(buf, n_mat, n_out, k, 3, 77)
+        assert np.array_equal(buf.download(np.uint8, n), hip.synth_q4_host(n_mat, n_out, k, 3, 77))
+
+
+@pytest.mark.parametrize("fmt,n_out,k", [(hip.PACK_GATE_UP, 1408, 2816), (hip.PACK_ROWS32, 2816, 704),
+                                         (hip.PACK_GATE_UP, 128, 256), (hip.PACK_ROWS32, 64, 64)])
+def test_pack_layout(gpu, fmt, n_out, k):
+    rows = rand_q4(np.random.default_rng(n_out + k), n_out, k)
+    dst = packed(rows, n_out, k, fmt)
+    assert np.array_equal(dst.download(np.uint8, rows.size), pack_np(rows, n_out, k, fmt))
+
+
+def test_quantize_q8_0_bitexact(gpu, orc):
+    rng = np.random.default_rng(21)
+    rows, k = 7, 2816
+    x = (rng.standard_normal((rows, k)) * rng.uniform(1e-6, 1e4, (rows, 1))).astype(np.float32)
+    x[0, :32] = 0.0                                    # zero block
+    x[1, :32] = 0.0
+    x[1, 0] = 127.0
+    x[1, 1:9] = [2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 126.5, -126.5]  # exact ties
+    x[2, 5] = np.nan                                   # NaN ignored by amax, quantised to 0
+    x[3, 40] = np.inf                                  # d = inf
+    x[4, 64:96] = rng.standard_normal(32) * 1e-40      # subnormal inputs, subnormal f16 scale
+    x[5, 96:128] = rng.standard_normal(32) * 3e7       # f16 scale overflow to inf
+    xd, q = dev(x), DevBuf(rows * (k // QK) * Q8B)
+    hip.quantize_q8_0(xd, q, rows, k)
+    got = q.download(np.uint8, rows * (k // QK) * Q8B).reshape(rows, -1)
+    for r in range(rows):
+        assert np.array_equal(got[r], orc.quantize_q8_0(x[r])), r
+
+
+@pytest.mark.parametrize("fmt,n_out,k", [(hip.PACK_GATE_UP, 1408, 2816), (hip.PACK_ROWS32, 2816, 704)])
+def test_block_sums_bitexact(gpu, orc, fmt, n_out, k):
+    rng = np.random.default_rng(k)
+    rows = rand_q4(rng, n_out, k)
+    xq = orc.quantize_q8_0(rng.standard_normal(k).astype(np.float32) * 3)
+    # extremes: every weight -8 against activations of +-127 (runtime/src/expert_kernel.rs:322-326)
+    rows2 = rows.copy().reshape(n_out, -1, Q4B)
+    rows2[:, :, 2:] = 0
+    xq2 = xq.copy().reshape(-1, Q8B)
+    xq2[::2, 2:] = 0x81
+    xq2[1::2, 2:] = 0x7F
+    for w_rows, a in ((rows, xq), (rows2.reshape(-1), xq2.reshape(-1))):
+        wd = packed(w_rows, n_out, k, fmt)
+        sums = DevBuf(n_out * (k // QK) * 4)
+        hip.q4q8_block_sums(wd, fmt, dev(a), sums, n_out, k)
+        got = sums.download(np.int32, n_out * (k // QK)).reshape(n_out, -1)
+        rb = w_rows.reshape(n_out, -1)
+        want = np.stack([orc.q4q8_block_sums(rb[r], a, k) for r in range(n_out)])
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("fmt,n_out,k", [(hip.PACK_GATE_UP, 1408, 2816), (hip.PACK_ROWS32, 2816, 704),
+                                         (hip.PACK_GATE_UP, 128, 256)])
+def test_q4q8_mm_matches_oracle_and_is_batch_invariant(gpu, orc, fmt, n_out, k):
+    rng = np.random.default_rng(n_out * 7 + k)
+    rows = rand_q4(rng, n_out, k)
+    wd = packed(rows, n_out, k, fmt)
+    n_in = 8
+    x = rng.standard_normal((n_in, k)).astype(np.float32)
+    xq = np.concatenate([orc.quantize_q8_0(x[t]) for t in range(n_in)])
+    y = DevBuf(n_in * n_out * 4)
+    hip.q4q8_mm(wd, fmt, dev(xq), y, n_out, k, n_in)
+    got = y.download(np.float32, n_in * n_out).reshape(n_in, n_out)
+    rb = rows.reshape(n_out, -1)
+    qb = xq.reshape(n_in, -1)
+    want = np.array([[orc.dot_q8_scalar(rb[r], qb[t], k) for r in range(n_out)] for t in range(n_in)], np.float32)
+    assert np.max(np.abs(got - want)) <= 1e-3 * rms(want)
+    # the reference's per-row summation bound
+    deq = np.stack([orc.dequant_q4_0(rb[r], k) for r in range(n_out)]).astype(np.float64)
+    for t in range(n_in):
+        xd = qb[t].reshape(-1, Q8B)
+        xv = (xd[:, 2:].view(np.int8).astype(np.float64) * xd[:, :2].copy().view(np.float16).astype(np.float64))
+        mag = np.abs(deq * xv.reshape(1, -1)).sum(axis=1)
+        assert np.all(np.abs(got[t] - want[t]) <= 4e-6 * mag + 1e-30)
+    y1 = DevBuf(n_out * 4)
+    hip.q4q8_mm(wd, fmt, dev(qb[n_in - 1]), y1, n_out, k, 1)
+    assert np.array_equal(y1.download(np.float32, n_out), got[n_in - 1])
+
+
+def test_geglu_q8_0(gpu, orc):
+    rng = np.random.default_rng(31)
+    rows, ff = 24, 704
+    gu = (rng.standard_normal((rows, 2 * ff)) * 2).astype(np.float32)
+    hq = DevBuf(rows * (ff // QK) * Q8B)
+    hip.geglu_q8_0(dev(gu), hq, rows, ff)
+    got = hq.download(np.uint8, rows * (ff // QK) * Q8B).reshape(rows, -1)
+    mism = 0
+    for r in range(rows):
+        h = np.array([orc.gelu(float(g)) for g in gu[r, :ff]], np.float32) * gu[r, ff:]
+        want = orc.quantize_q8_0(h)
+        dq = lambda b: (b.reshape(-1, Q8B)[:, 2:].view(np.int8).astype(np.float32) *
+                        b.reshape(-1, Q8B)[:, :2].copy().view(np.float16).astype(np.float32))
+        assert np.max(np.abs(dq(got[r]) - dq(want))) <= 1e-3 * rms(h) + 1e-2 * np.abs(h).max() / 127
+        mism += int((got[r] != want).sum())
+    assert mism <= rows * ff // 100  # tanhf differs by ulps across libms; quants rarely move
+
+
+def test_reference_ops(gpu, orc):
+    rng = np.random.default_rng(41)
+    # rvh_q4_mm against ops::matmul_q4_0 (runtime/tests/hip_ops.rs:56-81): rel L2 < 1e-5, batch invariance
+    for n_out, k in [(1408, 2816), (2816, 704)]:
+        for n_in in [1, 7]:
+            w = rand_q4(rng, n_out, k, 0.01, 0.03)
+            x = rng.uniform(-1, 1, (n_in, k)).astype(np.float32)
+            want = orc.matmul_q4_0(w, k, x, n_in, n_out)
+            y = DevBuf(n_in * n_out * 4)
+            wd = dev(w)
+            hip.q4_mm(wd, dev(x), y, n_out, k, n_in)
+            got = y.download(np.float32, n_in * n_out).reshape(n_in, n_out)
+            rel = np.sqrt(((got - want).astype(np.float64) ** 2).sum() / (want.astype(np.float64) ** 2).sum())
+            assert rel < 1e-5
+            if n_in > 1:
+                y1 = DevBuf(n_out * 4)
+                hip.q4_mm(wd, dev(x[-1]), y1, n_out, k, 1)
+                assert np.array_equal(y1.download(np.float32, n_out), got[-1])
+    # rvh_geglu_split rel < 1e-6 and rvh_moe_combine bitwise (runtime/tests/hip_ops.rs:402-439)
+    e, fe, used, n = 2816, 704, 8, 3
+    pairs = n * used
+    gu = rng.uniform(-2, 2, (pairs, 2 * fe)).astype(np.float32)
+    want_h = np.array([[orc.gelu(float(g)) for g in r[:fe]] for r in gu], np.float32) * gu[:, fe:]
+    h = DevBuf(pairs * fe * 4)
+    hip.geglu_split(dev(gu), h, pairs, fe)
+    got_h = h.download(np.float32, pairs * fe).reshape(pairs, fe)
+    assert np.sqrt(((got_h - want_h) ** 2).sum() / (want_h ** 2).sum()) < 1e-6
+    y = rng.uniform(-1, 1, (pairs, e)).astype(np.float32)
+    pos = np.arange(pairs, dtype=np.int32)[::-1].copy()
+    scale = rng.uniform(-1, 1, pairs).astype(np.float32)
+    weight = rng.uniform(-1, 1, pairs).astype(np.float32)
+    want = np.zeros((n, e), np.float32)
+    for t in range(n):
+        for j in range(used):
+            p = t * used + j
+            c = (y[pos[p]] * scale[p]) * weight[p]
+            want[t] = c if j == 0 else want[t] + c
+    out = DevBuf(n * e * 4)
+    hip.moe_combine(dev(y), pairs, dev(pos), dev(scale), dev(weight), out, n, used, e)
+    assert np.array_equal(out.download(np.float32, n * e).reshape(n, e), want)
+    # rvh_rms_norm, rvh_f32_mm, rvh_gather_rows
+    xr = rng.standard_normal((3, e)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, e).astype(np.float32)
+    o = DevBuf(3 * e * 4)
+    hip.rms_norm(dev(xr), o, dev(g), 3, e, 1e-6, 0.5)
+    got = o.download(np.float32, 3 * e).reshape(3, e)
+    for t in range(3):
+        assert np.max(np.abs(got[t] - orc.rms_norm(xr[t], g, 1e-6, 0.5))) <= 2e-6 * np.abs(got[t]).max()
+    wr = (rng.standard_normal((128, e)) * 0.02).astype(np.float32)
+    lg = DevBuf(3 * 128 * 4)
+    hip.f32_mm(dev(wr), dev(xr), lg, 128, e, 3)
+    got = lg.download(np.float32, 3 * 128).reshape(3, 128)
+    for t in range(3):
+        assert np.max(np.abs(got[t] - orc.matvec_f32(wr, xr[t]))) <= 1e-5
+    idx = np.array([2, 0, 2, 1], np.int32)
+    dst = DevBuf(4 * e * 4)
+    hip.gather_rows(dev(xr), 3, dev(idx), dst, 4, e)
+    assert np.array_equal(dst.download(np.float32, 4 * e).reshape(4, e), xr[idx])
+
+
+def test_out_of_range_calls_are_refused(gpu):
+    small = DevBuf(64)
+    with pytest.raises(hip.BoundsError):
+        hip.q4_mm(small, small, small, 1 << 20, 2816, 1)
+    with pytest.raises(hip.DeviceError) as e:
+        hip.check(hip.lib().rvm_q4q8_mm(small.ptr, 9, small.ptr, small.ptr, 64, 64, 1))
+    assert e.value.code == 1

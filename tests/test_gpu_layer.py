@@ -1,0 +1,246 @@
+"""End-to-end parity of the MoE layer on the GPU against the CPU oracle.
+
+Rules: top-k expert ids are bit-exact; f32 outputs agree within max-abs 1e-3 of the output's RMS.
+Workloads are the seeded synthetic configurations at the reference's shapes (128 experts, top-8,
+d = 2816, ff = 704): single-token decode, a ragged 32-token decode batch with Zipf(1.1)
+popularity, a 512-token prefill, and a teacher-forced multi-layer stack with router bias and
+an RMSNorm between layers. Size-independent properties (batch invariance, graph replays) cover
+what the oracle is too slow to check in full.
+"""
+import numpy as np
+import pytest
+
+from rosevine_amd import hip, moe, synth
+from rosevine_amd.hip import DevBuf
+
+pytestmark = pytest.mark.gpu
+
+N_EXP, TOP_K, D, FF = synth.N_EXP, synth.TOP_K, synth.D, synth.FF
+SEED = 0
+
+
+def dev(a):
+    return DevBuf.from_array(np.ascontiguousarray(a))
+
+
+def rms(a):
+    return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
+
+
+class HostExperts(dict):
+    """Reference-layout Q4_0 experts regenerated on the host on first use."""
+
+    def __init__(self, seed, stream0, n_out, k):
+        super().__init__()
+        self.args = (seed, stream0, n_out, k)
+
+    def __missing__(self, e):
+        seed, stream0, n_out, k = self.args
+        v = synth.host_expert(seed, stream0, int(e), n_out, k)
+        self[e] = v
+        return v
+
+
+_layers = {}
+
+
+def get_layer(layer=0, bias=False, ds=False):
+    key = (layer, bias, ds)
+    if key not in _layers:
+        router = synth.router_weights(SEED, layer)
+        b = synth.router_bias(SEED, layer) if bias else None
+        dsc = np.random.default_rng([SEED, layer, 9]).uniform(0.5, 1.5, N_EXP).astype(np.float32) if ds else None
+        L = moe.MoeLayer(N_EXP, TOP_K, D, FF, router, b, dsc)
+        L.synth_weights(SEED, synth.gate_up_stream(layer), synth.down_stream(layer))
+        gu = HostExperts(SEED, synth.gate_up_stream(layer), 2 * FF, D)
+        dn = HostExperts(SEED, synth.down_stream(layer), D, FF)
+        _layers[key] = (L, router, b, dsc, gu, dn)
+    return _layers[key]
+
+
+def oracle_layer(orc, key, x, pre_norm=False):
+    L, router, b, dsc, gu, dn = key
+    xin = np.stack([orc.rms_norm(r, None, 1e-6) for r in x]) if pre_norm else x
+    lg = orc.router_logits(router, b, xin, N_EXP, D)
+    ids, w, _ = orc.select_experts(lg, TOP_K)
+    for e in set(int(v) for v in ids.reshape(-1)):
+        gu[e], dn[e]
+    out = orc.experts_q8(gu, dn, dsc, xin, D, FF, ids, w, N_EXP)
+    return ids, w, out, lg
+
+
+def test_router_certified_ids_match_oracle(gpu, orc):
+    for bias in (False, True):
+        key = get_layer(0, bias=bias)
+        L, router, b = key[0], key[1], key[2]
+        n = 1024
+        x = synth.tokens(SEED + 1, n)
+        ws = moe.Workspace(L, n)
+        ids, w, lg = moe.router_select(L, dev(x), n, ws, with_logits=True)
+        want_lg = orc.router_logits(router, b, x, N_EXP, D)
+        want_ids, want_w, _ = orc.select_experts(want_lg, TOP_K)
+        assert np.array_equal(ids, want_ids.astype(np.int32))
+        assert np.max(np.abs(w - want_w)) <= 1e-5
+        print(f"[router] bias={bias} tokens={n} exactness fallbacks={ws.fallbacks()}", flush=True)
+        # the reference-order path: logits bit-exact, same ids
+        ws2 = moe.Workspace(L, n)
+        ids2, w2, lg2 = moe.router_select(L, dev(x), n, ws2, flags=hip.EXACT_SELECT, with_logits=True)
+        assert np.array_equal(lg2, want_lg)
+        assert np.array_equal(ids2, want_ids.astype(np.int32))
+        assert np.max(np.abs(w2 - want_w)) <= 2e-7
+        assert ws2.fallbacks() == n
+
+
+def test_router_ties_go_to_the_lower_index(gpu, orc):
+    rng = np.random.default_rng(5)
+    router = (rng.standard_normal((N_EXP, D)) * 0.02).astype(np.float32)
+    router[[7, 50, 51]] = router[3]          # identical logits: only the index can order them
+    router[[90, 91]] = router[12]
+    L = moe.MoeLayer(N_EXP, TOP_K, D, FF, router)
+    n = 256
+    x = synth.tokens(7, n)
+    ws = moe.Workspace(L, n)
+    ids, w = moe.router_select(L, dev(x), n, ws)
+    want_ids, want_w, _ = orc.select_experts(orc.router_logits(router, None, x, N_EXP, D), TOP_K)
+    assert np.array_equal(ids, want_ids.astype(np.int32))
+    assert np.max(np.abs(w - want_w)) <= 1e-5
+    assert ws.fallbacks() > 0
+
+
+def test_plan_matches_oracle(gpu, orc):
+    rng = np.random.default_rng(6)
+    for n_pairs in [8, 256, 3000, 4096]:
+        ids = (rng.zipf(1.2, n_pairs) % N_EXP).astype(np.int32)
+        order, pos_of, gs = DevBuf(n_pairs * 4), DevBuf(n_pairs * 4), DevBuf((N_EXP + 1) * 4)
+        hip.moe_plan(dev(ids), n_pairs, N_EXP, order, pos_of, gs)
+        o, p, g = orc.moe_plan(ids.astype(np.uint32), N_EXP)
+        assert np.array_equal(order.download(np.int32, n_pairs), o.astype(np.int32))
+        assert np.array_equal(pos_of.download(np.int32, n_pairs), p.astype(np.int32))
+        assert np.array_equal(gs.download(np.int32, N_EXP + 1), g.astype(np.int32))
+    # ids outside [0, n_exp) are left out of the plan
+    ids = np.array([3, -1, 3, 200, 0], np.int32)
+    order, pos_of, gs = DevBuf(20), DevBuf(20), DevBuf((N_EXP + 1) * 4)
+    hip.moe_plan(dev(ids), 5, N_EXP, order, pos_of, gs)
+    assert list(pos_of.download(np.int32, 5)) == [1, -1, 2, -1, 0]
+    assert list(order.download(np.int32, 3)) == [4, 0, 2]
+    assert gs.download(np.int32, N_EXP + 1)[-1] == 3
+
+
+@pytest.mark.parametrize("bias,ds,pre", [(False, False, False), (True, True, True)])
+def test_decode_matches_oracle(gpu, orc, bias, ds, pre):
+    key = get_layer(0, bias=bias, ds=ds)
+    L = key[0]
+    n = 16
+    x = synth.tokens(SEED + 2, n)
+    ids_ref, _, out_ref, _ = oracle_layer(orc, key, x, pre_norm=pre)
+    ws = moe.Workspace(L, 1)
+    xd, out = dev(x), DevBuf(n * D * 4)
+    flags = hip.PRE_NORM if pre else 0
+    for t in range(n):
+        moe.decode(L, xd, out, ws, flags=flags, x_off=t * D * 4, out_off=t * D * 4)
+    got = out.download(np.float32, n * D).reshape(n, D)
+    ids_dev = ws.selection(L, 1)[0][0]  # last token's selection
+    assert np.array_equal(ids_dev, ids_ref[-1].astype(np.int32))
+    for t in range(n):
+        assert np.max(np.abs(got[t] - out_ref[t])) <= 1e-3 * rms(out_ref[t]), t
+
+
+def test_forward_ragged_zipf_matches_oracle_and_decode(gpu, orc):
+    rng = np.random.default_rng(8)
+    router = synth.router_weights(SEED, 0)
+    bias = synth.zipf_bias(SEED)
+    L = moe.MoeLayer(N_EXP, TOP_K, D, FF, router, bias)
+    L.synth_weights(SEED, synth.gate_up_stream(0), synth.down_stream(0))
+    key = (L, router, bias, None, HostExperts(SEED, synth.gate_up_stream(0), 2 * FF, D),
+           HostExperts(SEED, synth.down_stream(0), D, FF))
+    n = 32
+    x = synth.tokens(SEED + 3, n)
+    ids_ref, _, out_ref, _ = oracle_layer(orc, key, x)
+    distinct = len(set(ids_ref.reshape(-1).tolist()))
+    print(f"[forward] 32 tokens, {distinct} distinct experts, max group {np.bincount(ids_ref.reshape(-1)).max()}",
+          flush=True)
+    ws = moe.Workspace(L, n)
+    xd, out = dev(x), DevBuf(n * D * 4)
+    moe.forward(L, xd, out, n, ws)
+    got = out.download(np.float32, n * D).reshape(n, D)
+    for t in range(n):
+        assert np.max(np.abs(got[t] - out_ref[t])) <= 1e-3 * rms(out_ref[t]), t
+    # batch invariance: each token's row equals its single-token decode bitwise
+    ws1, o1 = moe.Workspace(L, 1), DevBuf(D * 4)
+    for t in [0, 13, 31]:
+        moe.decode(L, xd, o1, ws1, x_off=t * D * 4)
+        assert np.array_equal(o1.download(np.float32, D), got[t]), t
+    del rng
+
+
+def test_prefill_512_is_batch_invariant(gpu, orc):
+    key = get_layer(0)
+    L = key[0]
+    n = 512
+    x = synth.tokens(SEED + 4, n)
+    ws = moe.Workspace(L, n)
+    xd, out = dev(x), DevBuf(n * D * 4)
+    moe.forward(L, xd, out, n, ws)
+    got = out.download(np.float32, n * D).reshape(n, D)
+    ws1, o1 = moe.Workspace(L, 1), DevBuf(D * 4)
+    for t in range(0, n, 37):
+        moe.decode(L, xd, o1, ws1, x_off=t * D * 4)
+        assert np.array_equal(o1.download(np.float32, D), got[t]), t
+    sub = [0, 255, 511]
+    _, _, out_ref, _ = oracle_layer(orc, key, x[sub])
+    for i, t in enumerate(sub):
+        assert np.max(np.abs(got[t] - out_ref[i])) <= 1e-3 * rms(out_ref[i]), t
+
+
+def test_graph_replays_match_eager(gpu):
+    key = get_layer(0)
+    L = key[0]
+    n = 4
+    x = synth.tokens(SEED + 5, n)
+    xd = dev(x)
+    ws = moe.Workspace(L, 1)
+    eager = DevBuf(n * D * 4)
+    for t in range(n):
+        moe.decode(L, xd, eager, ws, x_off=t * D * 4, out_off=t * D * 4)
+    want = eager.download(np.float32, n * D)
+    s = hip.Stream()
+    s.use()
+    try:
+        out = DevBuf(n * D * 4)
+        hip.Graph.begin()
+        for t in range(n):
+            moe.decode(L, xd, out, ws, x_off=t * D * 4, out_off=t * D * 4)
+        g = hip.Graph.end()
+        for rep in range(3):
+            out.upload(np.zeros(n * D, np.float32))
+            g.launch()
+            assert np.array_equal(out.download(np.float32, n * D), want), rep
+            moe.decode(L, xd, eager, ws)  # eager work between replays
+            hip.sync()
+        g.close()
+    finally:
+        hip.Stream.use_default()
+        hip.sync()
+        s.close()
+
+
+def test_stack_teacher_forced(gpu, orc):
+    """Three layers with router bias and RMSNorm between layers: each layer's ids are exact and
+    its output within tolerance, given the previous layer's device output as input."""
+    x = synth.tokens(SEED + 6, 4)
+    cur = x
+    for layer in range(3):
+        key = get_layer(layer, bias=True)
+        L = key[0]
+        pre = layer > 0
+        ids_ref, _, out_ref, _ = oracle_layer(orc, key, cur, pre_norm=pre)
+        ws = moe.Workspace(L, 4)
+        xd, out = dev(cur), DevBuf(4 * D * 4)
+        moe.forward(L, xd, out, 4, ws, flags=hip.PRE_NORM if pre else 0)
+        got = out.download(np.float32, 4 * D).reshape(4, D)
+        ids_dev = ws.selection(L, 4)[0]
+        assert np.array_equal(ids_dev, ids_ref.astype(np.int32)), layer
+        for t in range(4):
+            assert np.max(np.abs(got[t] - out_ref[t])) <= 1e-3 * rms(out_ref[t]), (layer, t)
+        cur = got
+
