@@ -233,6 +233,12 @@ float orc_gelu(float x) {
     return 0.5f * x * (1.0f + tanhf(inner));
 }
 
+/* runtime/src/exec.rs:606-611 */
+void orc_geglu_split(const float *gu, float *out, size_t rows, size_t ff) {
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t j = 0; j < ff; ++j) out[r * ff + j] = orc_gelu(gu[r * 2 * ff + j]) * gu[r * 2 * ff + ff + j];
+}
+
 /* runtime/src/ops.rs:170-179 */
 void orc_softmax(float *x, size_t n) {
     float max = -INFINITY;

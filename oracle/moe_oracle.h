@@ -48,6 +48,8 @@ void orc_matvec_f32(const float *w, size_t k, const float *x, float *y, size_t n
 void orc_rms_norm(float *x, const float *weight, size_t n, float eps, float post);
 /* runtime/src/ops.rs:145-149 */
 float orc_gelu(float x);
+/* runtime/src/exec.rs:606-611: out[r][j] = gelu(gu[r][j]) * gu[r][ff + j] for rows of 2*ff. */
+void orc_geglu_split(const float *gu, float *out, size_t rows, size_t ff);
 /* runtime/src/ops.rs:170-179 */
 void orc_softmax(float *x, size_t n);
 /* runtime/src/ops.rs:182-187 */

@@ -55,6 +55,7 @@ def _declare(L):
         "orc_rms_norm": (None, [vp, vp, sz, f32, f32]),
         "orc_gelu": (f32, [f32]),
         "orc_softmax": (None, [vp, sz]),
+        "orc_geglu_split": (None, [vp, vp, sz, sz]),
         "orc_top_k": (None, [vp, sz, sz, vp]),
         "orc_router_logits": (None, [vp, vp, vp, sz, sz, sz, vp]),
         "orc_select_experts": (None, [vp, sz, sz, sz, vp, vp]),
@@ -149,6 +150,13 @@ def rms_norm(x, weight=None, eps=1e-6, post=1.0) -> np.ndarray:
 
 def gelu(x: float) -> float:
     return lib().orc_gelu(x)
+
+
+def geglu_split(gu, ff) -> np.ndarray:
+    gu = _f32(gu).reshape(-1, 2 * ff)
+    out = np.empty((gu.shape[0], ff), np.float32)
+    lib().orc_geglu_split(_p(gu), _p(out), gu.shape[0], ff)
+    return out
 
 
 def softmax(x) -> np.ndarray:

@@ -4,129 +4,148 @@
 //
 //   router (router.hip)       -> ids, weights, Q8_0 activation blocks per token
 //   k_plan (router.hip)       -> pairs stably grouped by expert: order, pos_of, group starts
-//   k_gateup_grouped          -> per (expert, 64-row tile): each weight step is loaded once and
-//                                applied to up to TB tokens of the group; GeGLU + Q8_0 epilogue
-//   k_down_grouped            -> per (expert, 32-row tile): y rows of every pair of the group
+//   k_gateup_grouped          -> per (expert, 64-row tile): the tile's weights are loaded into
+//                                registers once and applied to every token of the group, TB at a
+//                                time; sequential block fold, GeGLU + Q8_0 epilogue per token
+//   k_down_grouped            -> per (expert, four 32-row tiles): y rows of every pair of the group
 //   k_combine_pairs           -> out[t] = sum_j (y[pos_of[t*k+j]] * scale) * weight, slot order
+// Each token's arithmetic is the decode kernels' (same split of K, same order), so a token's
+// result does not depend on the batch it arrives in.
 #include "internal.hpp"
 
 namespace rvm {
 
-constexpr int G_WAVES = 4;
-constexpr int G_CHUNK = 11;
-constexpr int TB = 4;  // tokens per pass over a weight tile
+constexpr int G_WAVES = 8;  // K split of a gate_up tile (as k_gateup_decode)
+constexpr int TB = 4;       // tokens per pass
 
+// Staging of n uint4 from global to LDS in two steps, so that a kernel can issue these loads
+// before its weight loads (the memory counter drains in order) and store them after: the source
+// index is clamped so that the loads need no branch.
+template <int MAXN, int NT>
+struct StageG {
+    static constexpr int IT = (MAXN + NT - 1) / NT;
+    static constexpr int SLOTS = IT * NT;  // LDS uint4 the destination must provide
+    uint4 v[IT];
+    __device__ __forceinline__ void load(const uint4 *__restrict__ src, int n) {
+#pragma unroll
+        for (int i = 0; i < IT; ++i) v[i] = src[min((int)threadIdx.x + i * NT, n - 1)];
+    }
+    // Unconditional: entries past n repeat the last one, so the loads never sink into a branch.
+    __device__ __forceinline__ void store(uint4 *dst) const {
+#pragma unroll
+        for (int i = 0; i < IT; ++i) dst[threadIdx.x + i * NT] = v[i];
+    }
+};
+
+template <int PER>
+__device__ __forceinline__ void lane_terms_g(const uint4 (&wv)[PER], const uint32_t (&sv)[PER], const uint4 *act,
+                                             float (&t)[PER]) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const uint4 a0 = act[i * 3], a1 = act[i * 3 + 1];
+        const float dx = __builtin_bit_cast(float, act[i * 3 + 2].x);
+        const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        t[i] = block_term(block_dot(wv[i], a), h2f((uint16_t)sv[i]), dx);
+    }
+}
+
+template <int PER>
 __global__ __launch_bounds__(G_WAVES * 64) void k_gateup_grouped(
     const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl, const int32_t *__restrict__ gstart,
-    const int32_t *__restrict__ order, const uint32_t *__restrict__ xact, uint32_t *__restrict__ hact, int T, int S,
+    const int32_t *__restrict__ order, const uint4 *__restrict__ xact, uint32_t *__restrict__ hact, int T,
     int top_k) {
-    __shared__ float part[G_WAVES][TB][64];
+    constexpr int S = PER * G_WAVES;
+    using St = StageG<S * 3, G_WAVES * 64>;
+    __shared__ uint4 act[TB][St::SLOTS];
+    __shared__ float terms[64][S + 1];
     const int t = blockIdx.x, e = blockIdx.y;
     const int g0 = gstart[e], g1 = gstart[e + 1];
     if (g0 >= g1) return;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int per = S / G_WAVES;
-    const int s0 = w * per;
-    const size_t base = ((size_t)e * T + t) * S + s0;
-    const uint4 *np = nib + base * 64 + lane;
-    const uint16_t *sp = scl + base * 64 + lane;
+    const size_t base = (((size_t)e * T + t) * S + (size_t)w * PER) * 64 + lane;
+    uint4 wv[PER];
+    uint32_t sv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        wv[i] = nib[base + (size_t)i * 64];
+        sv[i] = scl[base + (size_t)i * 64];
+    }
     for (int k0 = g0; k0 < g1; k0 += TB) {
         const int nt = min(TB, g1 - k0);
-        const uint32_t *ap[TB];
+        St st[TB];
 #pragma unroll
-        for (int i = 0; i < TB; ++i) {
-            const int tok = order[k0 + (i < nt ? i : 0)] / top_k;
-            ap[i] = xact + ((size_t)tok * S + s0) * ACT_DW;  // xact is [token][S blocks]
-        }
-        float acc[TB] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int c = 0; c < per; c += G_CHUNK) {
-            uint4 wv[G_CHUNK];
-            uint16_t sv[G_CHUNK];
-#pragma unroll
-            for (int i = 0; i < G_CHUNK; ++i)
-                if (c + i < per) {
-                    wv[i] = np[(size_t)(c + i) * 64];
-                    sv[i] = sp[(size_t)(c + i) * 64];
-                }
-#pragma unroll
-            for (int i = 0; i < G_CHUNK; ++i)
-                if (c + i < per) {
-                    const float dw = h2f(sv[i]);
-#pragma unroll
-                    for (int q = 0; q < TB; ++q)
-                        if (q < nt) {
-                            const uint32_t *a = ap[q] + (c + i) * ACT_DW;
-                            const int sumi = block_dot(wv[i], a);
-                            acc[q] = fmaf((float)sumi, dw * __builtin_bit_cast(float, a[8]), acc[q]);
-                        }
-                }
+        for (int q = 0; q < TB; ++q) {
+            const int tok = order[k0 + (q < nt ? q : 0)] / top_k;
+            st[q].load(xact + (size_t)tok * S * 3, S * 3);
         }
 #pragma unroll
-        for (int q = 0; q < TB; ++q) part[w][q][lane] = acc[q];
+        for (int q = 0; q < TB; ++q) st[q].store(act[q]);
         __syncthreads();
-        if (w == 0) {
-            for (int q = 0; q < nt; ++q) {
-                float y = part[0][q][lane];
+        for (int q = 0; q < nt; ++q) {
+            float tv[PER];
+            lane_terms_g<PER>(wv, sv, act[q] + w * PER * 3, tv);
 #pragma unroll
-                for (int i = 1; i < G_WAVES; ++i) y += part[i][q][lane];
+            for (int i = 0; i < PER; ++i) terms[lane][w * PER + i] = tv[i];
+            __syncthreads();
+            if (w == 0) {
+                float y = 0.0f;  // sequential fold of the row's block terms
+#pragma unroll 8
+                for (int b = 0; b < S; ++b) y = y + terms[lane][b];
                 const float up = __shfl_xor(y, 32);
                 const float h = gelu(y) * up;
                 uint16_t dbits;
                 const int qv = quant_q8_half(h, &dbits);
                 store_prep_half(qv, dbits, lane & 31, hact + ((size_t)(k0 + q) * T + t) * ACT_DW, lane < 32);
             }
+            __syncthreads();
         }
-        __syncthreads();
     }
 }
 
-__global__ __launch_bounds__(64) void k_down_grouped(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl,
-                                                     const int32_t *__restrict__ gstart,
-                                                     const uint32_t *__restrict__ hact, float *__restrict__ y, int T,
-                                                     int S, int d) {
-    const int t = blockIdx.x, e = blockIdx.y;
+template <int S>  // steps per lane = ff / 64
+__global__ __launch_bounds__(256) void k_down_grouped(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl,
+                                                      const int32_t *__restrict__ gstart,
+                                                      const uint4 *__restrict__ hact, float *__restrict__ y, int T,
+                                                      int d) {
+    constexpr int NB = 2 * S;
+    using St = StageG<NB * 3, 256>;
+    __shared__ uint4 act[TB][St::SLOTS];
+    const int e = blockIdx.y;
     const int g0 = gstart[e], g1 = gstart[e + 1];
     if (g0 >= g1) return;
-    const int lane = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + w;  // this wave's 32-row tile
     const int kp = lane >> 5;
-    const size_t base = ((size_t)e * T + t) * S;
-    const uint4 *np = nib + base * 64 + lane;
-    const uint16_t *sp = scl + base * 64 + lane;
-    const int nb = 2 * S;
+    const size_t base = ((size_t)e * T + t) * S * 64 + lane;
+    uint4 wv[S];
+    uint32_t sv[S];
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+        wv[i] = nib[base + (size_t)i * 64];
+        sv[i] = scl[base + (size_t)i * 64];
+    }
     for (int k0 = g0; k0 < g1; k0 += TB) {
         const int nt = min(TB, g1 - k0);
-        float acc[TB] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int c = 0; c < S; c += G_CHUNK) {
-            uint4 wv[G_CHUNK];
-            uint16_t sv[G_CHUNK];
+        St st[TB];
 #pragma unroll
-            for (int i = 0; i < G_CHUNK; ++i)
-                if (c + i < S) {
-                    wv[i] = np[(size_t)(c + i) * 64];
-                    sv[i] = sp[(size_t)(c + i) * 64];
-                }
+        for (int q = 0; q < TB; ++q) st[q].load(hact + (size_t)(k0 + (q < nt ? q : 0)) * NB * 3, NB * 3);
 #pragma unroll
-            for (int i = 0; i < G_CHUNK; ++i)
-                if (c + i < S) {
-                    const float dw = h2f(sv[i]);
-#pragma unroll
-                    for (int q = 0; q < TB; ++q)
-                        if (q < nt) {
-                            const uint32_t *a = hact + ((size_t)(k0 + q) * nb + kp * S + c + i) * ACT_DW;
-                            uint32_t av[9];
-#pragma unroll
-                            for (int r = 0; r < 9; ++r) av[r] = a[r];
-                            const int sumi = block_dot(wv[i], av);
-                            acc[q] = fmaf((float)sumi, dw * __builtin_bit_cast(float, av[8]), acc[q]);
-                        }
-                }
-        }
+        for (int q = 0; q < TB; ++q) st[q].store(act[q]);
+        __syncthreads();
 #pragma unroll
         for (int q = 0; q < TB; ++q) {
-            const float other = __shfl_xor(acc[q], 32);
-            if (q < nt && lane < 32) y[(size_t)(k0 + q) * d + (size_t)t * 32 + lane] = acc[q] + other;
+            float tv[S];
+            lane_terms_g<S>(wv, sv, act[q] + kp * S * 3, tv);
+            float acc = 0.0f;  // block order: this half, then the other half's terms
+#pragma unroll
+            for (int i = 0; i < S; ++i) acc = acc + tv[i];
+#pragma unroll
+            for (int i = 0; i < S; ++i) acc = acc + __shfl_xor(tv[i], 32);
+            if (q < nt && lane < 32) y[(size_t)(k0 + q) * d + (size_t)t * 32 + lane] = acc;
         }
+        __syncthreads();
     }
 }
 
@@ -153,7 +172,7 @@ using namespace rvm;
 
 extern "C" int rvm_moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int flags, float eps,
                                void *ws, size_t ws_bytes) {
-    RVM_CHECK(layer_ok(L) && x && out && ws && n_tok > 0 && n_tok <= 65535);
+    RVM_CHECK(layer_ok(L) && x && out && ws && n_tok > 0 && n_tok <= MAX_TOKENS);
     if (n_tok == 1) return rvm_moe_decode(L, x, out, flags, eps, ws, ws_bytes);
     const WsLayout lay = ws_layout(L, n_tok);
     RVM_CHECK(ws_bytes >= lay.total);
@@ -164,28 +183,34 @@ extern "C" int rvm_moe_forward(const rvm_layer *L, const float *x, float *out, i
     int32_t *pos_of = (int32_t *)(w + lay.pos_of);
     int32_t *gstart = (int32_t *)(w + lay.gstart);
     float *y = (float *)(w + lay.y);
-    uint32_t *xact = (uint32_t *)(w + lay.xact);
+    const uint4 *xact = (const uint4 *)(w + lay.xact);
     uint32_t *hact = (uint32_t *)(w + lay.hact);
     int rc = launch_router(L, x, n_tok, flags, eps, w, lay, ids, wts, nullptr);
     if (rc) return rc;
     const int pairs = n_tok * L->top_k;
     if ((rc = launch_plan(ids, pairs, L->n_exp, order, pos_of, gstart))) return rc;
 
-    const int Tg = 2 * L->ff / 64, Sg = L->d / QK;
-    const size_t gu_entries = (size_t)L->n_exp * 2 * L->ff * Sg;
+    const int Tg = 2 * L->ff / 64;
+    const size_t gu_entries = (size_t)L->n_exp * 2 * L->ff * (L->d / QK);
     const uint4 *gnib = (const uint4 *)L->gate_up;
     const uint16_t *gscl = (const uint16_t *)((const uint8_t *)L->gate_up + gu_entries * 16);
-    hipLaunchKernelGGL(k_gateup_grouped, dim3(Tg, L->n_exp), dim3(G_WAVES * 64), 0, cur_stream(), gnib, gscl, gstart,
-                       order, xact, hact, Tg, Sg, L->top_k);
-    if ((rc = launched())) return rc;
+    rc = with_steps(L->d / 256, [&](auto per) {
+        hipLaunchKernelGGL(k_gateup_grouped<decltype(per)::value>, dim3(Tg, L->n_exp), dim3(G_WAVES * 64), 0,
+                           cur_stream(), gnib, gscl, gstart, order, xact, hact, Tg, L->top_k);
+        return launched();
+    });
+    if (rc) return rc;
 
-    const int Td = L->d / 32, Sd = L->ff / 64;
+    const int Td = L->d / 32;  // a multiple of 8, so the four-tile groups cover it exactly
     const size_t dn_entries = (size_t)L->n_exp * L->d * (L->ff / QK);
     const uint4 *dnib = (const uint4 *)L->down;
     const uint16_t *dscl = (const uint16_t *)((const uint8_t *)L->down + dn_entries * 16);
-    hipLaunchKernelGGL(k_down_grouped, dim3(Td, L->n_exp), dim3(64), 0, cur_stream(), dnib, dscl, gstart, hact, y, Td,
-                       Sd, L->d);
-    if ((rc = launched())) return rc;
+    rc = with_steps(L->ff / 64, [&](auto s) {
+        hipLaunchKernelGGL(k_down_grouped<decltype(s)::value>, dim3(Td / 4, L->n_exp), dim3(256), 0, cur_stream(),
+                           dnib, dscl, gstart, (const uint4 *)hact, y, Td, L->d);
+        return launched();
+    });
+    if (rc) return rc;
 
     hipLaunchKernelGGL(k_combine_pairs, dim3(n_tok), dim3(256), 0, cur_stream(), y, pos_of, ids, wts, L->down_scale,
                        out, L->top_k, L->d);

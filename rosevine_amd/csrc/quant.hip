@@ -1,6 +1,7 @@
 // quant.hip - Q8_0 activation quantisation, GeGLU + Q8_0, and the generic packed Q4_0 x Q8_0
 // GEMV/GEMM with its per-block integer sums (runtime/src/ops.rs:95-105,
-// runtime/src/expert_kernel.rs:147-161, runtime/src/exec.rs:606-611).
+// runtime/src/expert_kernel.rs:147-161, runtime/src/exec.rs:606-611). All of them reproduce the
+// reference bit for bit on the same inputs.
 #include "internal.hpp"
 
 namespace rvm {
@@ -57,13 +58,16 @@ __device__ __forceinline__ float load_q8_block(const uint8_t *blk, uint32_t *q) 
     return h2f(h[0]);
 }
 
-// Generic packed GEMV/GEMM: one wave per (tile, token). For RVM_PACK_ROWS32 the two half-waves
-// hold the two halves of each row's blocks and are added (half 0 + half 1) at the end.
-// When sums != nullptr (n_in == 1) the per-block int32 sums are stored instead of y.
+// Generic packed GEMV/GEMM: one wave per (tile, token), each row's block terms folded in block
+// order as the reference's dot_q8_scalar. RVM_PACK_GATE_UP lanes own whole rows; for
+// RVM_PACK_ROWS32 the two half-waves own the two halves of each row's blocks, and their terms meet
+// in LDS (terms[32][nb + 1], dynamic) for the fold. When sums != nullptr (n_in == 1) the per-block
+// int32 sums are stored instead of y.
 __global__ __launch_bounds__(64) void k_q4q8_generic(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl,
                                                      const uint8_t *__restrict__ xq, float *__restrict__ y,
                                                      int32_t *__restrict__ sums, int n_out, int nb, int T, int S,
                                                      int format) {
+    extern __shared__ float terms[];
     const int t = blockIdx.x, tok = blockIdx.y, l = threadIdx.x;
     const uint8_t *xrow = xq + (size_t)tok * nb * Q8_BLOCK;
     float acc = 0.0f;
@@ -83,12 +87,19 @@ __global__ __launch_bounds__(64) void k_q4q8_generic(const uint4 *__restrict__ n
         prep_from_q8(q, a);
         const int sumi = block_dot(nib[e], a);
         if (sums) sums[(size_t)row * nb + b] = sumi;
-        acc = fmaf((float)sumi, h2f(scl[e]) * dx, acc);
+        const float term = block_term(sumi, h2f(scl[e]), dx);
+        if (format == RVM_PACK_GATE_UP)
+            acc = acc + term;
+        else
+            terms[(l & 31) * (nb + 1) + b] = term;
     }
     if (sums) return;
     if (format == RVM_PACK_ROWS32) {
-        const float other = __shfl_xor(acc, 32);
-        if (l < 32) y[(size_t)tok * n_out + row] = acc + other;
+        __syncthreads();
+        if (l < 32) {
+            for (int b = 0; b < nb; ++b) acc = acc + terms[l * (nb + 1) + b];
+            y[(size_t)tok * n_out + row] = acc;
+        }
     } else {
         y[(size_t)tok * n_out + row] = acc;
     }
@@ -104,7 +115,7 @@ static bool geo(int n_out, int k, int format, int *T, int *S) {
         return true;
     }
     if (format == RVM_PACK_ROWS32) {
-        if (n_out % 32 || nb % 2) return false;
+        if (n_out % 32 || nb % 2 || nb > 256) return false;
         *T = n_out / 32;
         *S = nb / 2;
         return true;
@@ -140,7 +151,8 @@ int rvm_q4q8_mm(const void *w_packed, int format, const void *xq, float *y, int 
     const size_t entries = (size_t)n_out * (k / QK);
     const uint4 *nib = (const uint4 *)w_packed;
     const uint16_t *scl = (const uint16_t *)((const uint8_t *)w_packed + entries * 16);
-    hipLaunchKernelGGL(k_q4q8_generic, dim3(T, n_in), dim3(64), 0, cur_stream(), nib, scl, (const uint8_t *)xq, y,
+    const size_t smem = format == RVM_PACK_ROWS32 ? (size_t)32 * (k / QK + 1) * 4 : 0;
+    hipLaunchKernelGGL(k_q4q8_generic, dim3(T, n_in), dim3(64), smem, cur_stream(), nib, scl, (const uint8_t *)xq, y,
                        (int32_t *)nullptr, n_out, k / QK, T, S, format);
     return launched();
 }
@@ -151,7 +163,8 @@ int rvm_q4q8_block_sums(const void *w_packed, int format, const void *xq, int32_
     const size_t entries = (size_t)n_out * (k / QK);
     const uint4 *nib = (const uint4 *)w_packed;
     const uint16_t *scl = (const uint16_t *)((const uint8_t *)w_packed + entries * 16);
-    hipLaunchKernelGGL(k_q4q8_generic, dim3(T, 1), dim3(64), 0, cur_stream(), nib, scl, (const uint8_t *)xq,
+    const size_t smem = format == RVM_PACK_ROWS32 ? (size_t)32 * (k / QK + 1) * 4 : 0;
+    hipLaunchKernelGGL(k_q4q8_generic, dim3(T, 1), dim3(64), smem, cur_stream(), nib, scl, (const uint8_t *)xq,
                        (float *)nullptr, sums, n_out, k / QK, T, S, format);
     return launched();
 }

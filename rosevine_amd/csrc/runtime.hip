@@ -10,6 +10,20 @@ static thread_local hipStream_t g_stream = nullptr;
 
 hipStream_t cur_stream() { return g_stream; }
 
+// LDS a workgroup may allocate on the current device, capped at the 64 KiB that needs no
+// per-kernel attribute.
+int max_lds_per_block() {
+    static int v = 0;
+    if (!v) {
+        int dev = 0, x = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&x, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || x <= 0)
+            x = 65536;
+        v = x < 65536 ? x : 65536;
+    }
+    return v;
+}
+
 // ---- synthetic Q4_0 weights: a counter-based generator, identical on host and device ----
 
 __host__ __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {

@@ -1,6 +1,9 @@
 """End-to-end parity of the MoE layer on the GPU against the CPU oracle.
 
 Rules: top-k expert ids are bit-exact; f32 outputs agree within max-abs 1e-3 of the output's RMS.
+The expert intermediates (gate/up rows, GeGLU, the Q8_0 down inputs, the down rows) are the
+reference's bits, so the outputs differ only through the last bits of the routing weights: the
+tests also hold them to 2e-5 of the RMS, which any quantisation flip would exceed.
 Workloads are the seeded synthetic configurations at the reference's shapes (128 experts, top-8,
 d = 2816, ff = 704): single-token decode, a ragged 32-token decode batch with Zipf(1.1)
 popularity, a 512-token prefill, and a teacher-forced multi-layer stack with router bias and
@@ -25,6 +28,12 @@ def dev(a):
 
 def rms(a):
     return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
+
+
+def assert_close(got, want, what):
+    err, r = float(np.max(np.abs(got - want))), rms(want)
+    assert err <= 1e-3 * r, f"{what}: max|diff| {err:.3g} > 1e-3 * rms {r:.3g}"
+    assert err <= 2e-5 * r, f"{what}: max|diff| {err:.3g} > 2e-5 * rms {r:.3g}"
 
 
 class HostExperts(dict):
@@ -142,7 +151,7 @@ def test_decode_matches_oracle(gpu, orc, bias, ds, pre):
     ids_dev = ws.selection(L, 1)[0][0]  # last token's selection
     assert np.array_equal(ids_dev, ids_ref[-1].astype(np.int32))
     for t in range(n):
-        assert np.max(np.abs(got[t] - out_ref[t])) <= 1e-3 * rms(out_ref[t]), t
+        assert_close(got[t], out_ref[t], f"token {t}")
 
 
 def test_forward_ragged_zipf_matches_oracle_and_decode(gpu, orc):
@@ -164,7 +173,7 @@ def test_forward_ragged_zipf_matches_oracle_and_decode(gpu, orc):
     moe.forward(L, xd, out, n, ws)
     got = out.download(np.float32, n * D).reshape(n, D)
     for t in range(n):
-        assert np.max(np.abs(got[t] - out_ref[t])) <= 1e-3 * rms(out_ref[t]), t
+        assert_close(got[t], out_ref[t], f"token {t}")
     # batch invariance: each token's row equals its single-token decode bitwise
     ws1, o1 = moe.Workspace(L, 1), DevBuf(D * 4)
     for t in [0, 13, 31]:
@@ -189,7 +198,7 @@ def test_prefill_512_is_batch_invariant(gpu, orc):
     sub = [0, 255, 511]
     _, _, out_ref, _ = oracle_layer(orc, key, x[sub])
     for i, t in enumerate(sub):
-        assert np.max(np.abs(got[t] - out_ref[i])) <= 1e-3 * rms(out_ref[i]), t
+        assert_close(got[t], out_ref[i], f"token {t}")
 
 
 def test_graph_replays_match_eager(gpu):
@@ -241,6 +250,6 @@ def test_stack_teacher_forced(gpu, orc):
         ids_dev = ws.selection(L, 4)[0]
         assert np.array_equal(ids_dev, ids_ref.astype(np.int32)), layer
         for t in range(4):
-            assert np.max(np.abs(got[t] - out_ref[t])) <= 1e-3 * rms(out_ref[t]), (layer, t)
+            assert_close(got[t], out_ref[t], f"layer {layer} token {t}")
         cur = got
 
