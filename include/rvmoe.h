@@ -54,6 +54,8 @@ int rvh_rms_norm(const float *x, float *out, const float *weight, int rows, int 
 int rvh_f32_mm(const float *w, const float *x, float *y, int n_out, int k, int n_in);
 /* y[t][r] = W_q4[r] . x[t], Q4_0 rows (reference layout), f32 activations; rvhip.h:44-45. */
 int rvh_q4_mm(const void *w, const float *x, float *y, int n_out, int k, int n_in);
+/* rvh_q4_mm's result up to summation order; x 16-byte aligned, w 2-byte aligned; rvhip.h:46-48. */
+int rvh_q4_mv(const void *w, const float *x, float *y, int n_out, int k, int n_in);
 /* Rows of 2*ff (gate then up) to rows of ff: gelu(gate) * up; rvhip.h:70-71. */
 int rvh_geglu_split(const float *gu, float *out, int rows, int ff);
 /* dst[i] = src[idx[i]], rows of width; rvhip.h:76-77. */

@@ -148,6 +148,13 @@ int rvh_q4_mm(const void *w, const float *x, float *y, int n_out, int k, int n_i
     return launched();
 }
 
+// The reference's K2 variant (rvhip.h:46-48) has rvh_q4_mm's result up to summation order and asks
+// for 16-byte aligned x and 2-byte aligned w; here it is the same kernel.
+int rvh_q4_mv(const void *w, const float *x, float *y, int n_out, int k, int n_in) {
+    RVM_CHECK(((uintptr_t)x & 15) == 0);
+    return rvh_q4_mm(w, x, y, n_out, k, n_in);
+}
+
 int rvh_geglu_split(const float *gu, float *out, int rows, int ff) {
     RVM_CHECK(gu && out && rows > 0 && ff > 0);
     const size_t n = (size_t)rows * ff;

@@ -76,6 +76,7 @@ SIGNATURES = {
     "rvh_rms_norm": (_i, [_vp, _vp, _vp, _i, _i, _f, _f]),
     "rvh_f32_mm": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "rvh_q4_mm": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "rvh_q4_mv": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "rvh_geglu_split": (_i, [_vp, _vp, _i, _i]),
     "rvh_gather_rows": (_i, [_vp, _vp, _vp, _i, _i]),
     "rvh_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
@@ -319,6 +320,14 @@ def f32_mm(w: DevBuf, x: DevBuf, y: DevBuf, n_out: int, k: int, n_in: int) -> No
 def q4_mm(w: DevBuf, x: DevBuf, y: DevBuf, n_out: int, k: int, n_in: int) -> None:
     check(lib().rvh_q4_mm(_need(w, n_out * (k // QK) * Q4_BLOCK), _need(x, n_in * k * 4),
                           _need(y, n_in * n_out * 4), n_out, k, n_in))
+
+
+def q4_mv(w: DevBuf, x: DevBuf, y: DevBuf, n_out: int, k: int, n_in: int) -> None:
+    """rvh_q4_mv; like the reference wrapper (runtime/src/hip.rs:384-392) it takes rvh_q4_mm for
+    activations that are not 16-byte aligned."""
+    wp, xp = _need(w, n_out * (k // QK) * Q4_BLOCK), _need(x, n_in * k * 4)
+    fn = lib().rvh_q4_mv if xp % 16 == 0 and wp % 2 == 0 else lib().rvh_q4_mm
+    check(fn(wp, xp, _need(y, n_in * n_out * 4), n_out, k, n_in))
 
 
 def geglu_split(gu: DevBuf, out: DevBuf, rows: int, ff: int) -> None:

@@ -23,7 +23,8 @@ def test_header_declares_the_reference_runtime_and_moe_entry_points():
               "rvh_event_sync", "rvh_event_elapsed"]:
         assert n in names
     # the reference's expert-path kernels (rvhip.h:42-80)
-    for n in ["rvh_rms_norm", "rvh_f32_mm", "rvh_q4_mm", "rvh_geglu_split", "rvh_gather_rows", "rvh_moe_combine"]:
+    for n in ["rvh_rms_norm", "rvh_f32_mm", "rvh_q4_mm", "rvh_q4_mv", "rvh_geglu_split", "rvh_gather_rows",
+              "rvh_moe_combine"]:
         assert n in names
     assert "rvm_moe_decode" in names and "rvm_moe_forward" in names
 

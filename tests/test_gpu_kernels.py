@@ -189,6 +189,12 @@ def test_reference_ops(gpu, orc):
                 y1 = DevBuf(n_out * 4)
                 hip.q4_mm(wd, dev(x[-1]), y1, n_out, k, 1)
                 assert np.array_equal(y1.download(np.float32, n_out), got[-1])
+            # rvh_q4_mv: the same result up to summation order (rvhip.h:46-48)
+            ymv = DevBuf(n_in * n_out * 4)
+            hip.q4_mv(wd, dev(x), ymv, n_out, k, n_in)
+            got_mv = ymv.download(np.float32, n_in * n_out).reshape(n_in, n_out)
+            rel = np.sqrt(((got_mv - want).astype(np.float64) ** 2).sum() / (want.astype(np.float64) ** 2).sum())
+            assert rel < 1e-5
     # rvh_geglu_split rel < 1e-6 and rvh_moe_combine bitwise (runtime/tests/hip_ops.rs:402-439)
     e, fe, used, n = 2816, 704, 8, 3
     pairs = n * used

@@ -48,8 +48,13 @@ def test_f32_to_f16_round_to_nearest_even_against_numpy(orc):
     rng = np.random.default_rng(11)
     # random bit patterns across the whole f32 range, plus every f16 midpoint neighbourhood
     xs = rng.integers(0, 2**32, 20000, dtype=np.uint64).astype(np.uint32).view(np.float32)
-    mids = (np.arange(0, 0x7C00, 7, dtype=np.uint32) << 13) + 0x1000  # exact ties of the 13 dropped bits
+    # exact midpoints between consecutive finite f16 values (normal and subnormal), representable
+    # in f32, and their f32 neighbours on either side
+    h = np.arange(0, 0x7BFF, dtype=np.uint16)
+    lo, hi = h.view(np.float16).astype(np.float64), (h + 1).view(np.float16).astype(np.float64)
+    mids = ((lo + hi) / 2).astype(np.float32).view(np.uint32)
     xs = np.concatenate([xs, mids.view(np.float32), (mids + 1).view(np.float32), (mids - 1).view(np.float32)])
+    xs = np.concatenate([xs, -xs])
     xs = xs[~np.isnan(xs)]
     with np.errstate(over="ignore"):
         want = xs.astype(np.float16).view(np.uint16)
@@ -370,7 +375,9 @@ def test_experts_q8_against_f64_pipeline(orc):
         y64 = (vals * dw * q[None] * dx).sum(axis=(1, 2))
         mag = (np.abs(vals * dw * q[None] * dx)).sum(axis=(1, 2))
         assert np.all(np.abs(y[k] - y64) <= 4e-6 * mag + 1e-30)
-    for t in range(n_tok):  # slot-order combine, first term assigned
+    # slot-order combine, first term assigned, (y * scale) * weight: the expected values of the
+    # reference's bitwise combine test (runtime/tests/hip_ops.rs:421-439)
+    for t in range(n_tok):
         o = None
         for j in range(used):
             p = t * used + j
