@@ -185,7 +185,7 @@ extern "C" int rvm_moe_forward(const rvm_layer *L, const float *x, float *out, i
     float *y = (float *)(w + lay.y);
     const uint4 *xact = (const uint4 *)(w + lay.xact);
     uint32_t *hact = (uint32_t *)(w + lay.hact);
-    int rc = launch_router(L, x, n_tok, flags, eps, w, lay, ids, wts, nullptr);
+    int rc = launch_router(L, x, n_tok, flags, eps, w, lay, ids, wts, nullptr, true);
     if (rc) return rc;
     const int pairs = n_tok * L->top_k;
     if ((rc = launch_plan(ids, pairs, L->n_exp, order, pos_of, gstart))) return rc;

@@ -19,6 +19,7 @@
 #include <type_traits>
 
 #include "../../include/rvmoe.h"
+#include "tanhf.hpp"
 
 namespace rvm {
 
@@ -88,111 +89,12 @@ __device__ __forceinline__ int sat_i8(float v) {
     return (int)v;
 }
 
-// expm1f and tanhf as the platform libm of the reference computes them: Rust's f32::tanh is the
-// C library's tanhf, which on the reference's Linux hosts (glibc 2.35) is the fdlibm algorithm
-// (Sun Microsystems; glibc sysdeps/ieee754/flt-32/s_tanhf.c and s_expm1f.c). The steps and
-// constants below are that published algorithm, evaluated with the same single-precision
-// operations, so the device result equals glibc's tanhf on every f32 input (compared over all
-// 2^32 inputs on the host; the GPU tests compare the device against the host libm).
-__host__ __device__ inline float fb_expm1f(float x) {
-    const float one = 1.0f, huge = 1.0e+30f, tiny = 1.0e-30f;
-    const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f, invln2 = 1.4426950216e+00f;
-    const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f,
-                Q4 = 4.0082177293e-06f, Q5 = -2.0109921195e-07f;
-    float y, hi, lo, c = 0.0f, t, e, hxs, hfx, r1;
-    int32_t k;
-    uint32_t hx = __builtin_bit_cast(uint32_t, x);
-    const uint32_t xsb = hx & 0x80000000u;
-    hx &= 0x7fffffffu;
-    if (hx >= 0x4195b844u) {  // |x| >= 27 ln2
-        if (hx >= 0x42b17218u) {
-            if (hx > 0x7f800000u) return x + x;
-            if (hx == 0x7f800000u) return xsb == 0 ? x : -1.0f;
-            if (xsb == 0 && hx > 0x42b17217u) return huge * huge;
-        }
-        if (xsb != 0) return tiny - one;
-    }
-    if (hx > 0x3eb17218u) {  // |x| > ln2 / 2: argument reduction
-        if (hx < 0x3F851592u) {
-            if (xsb == 0) {
-                hi = x - ln2_hi;
-                lo = ln2_lo;
-                k = 1;
-            } else {
-                hi = x + ln2_hi;
-                lo = -ln2_lo;
-                k = -1;
-            }
-        } else {
-            k = (int32_t)(invln2 * x + (xsb == 0 ? 0.5f : -0.5f));
-            t = (float)k;
-            hi = x - t * ln2_hi;
-            lo = t * ln2_lo;
-        }
-        x = hi - lo;
-        c = (hi - x) - lo;
-    } else if (hx < 0x33000000u) {  // |x| < 2^-25
-        t = huge + x;
-        return x - (t - (huge + x));
-    } else {
-        k = 0;
-    }
-    hfx = 0.5f * x;
-    hxs = x * hfx;
-    r1 = one + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
-    t = 3.0f - r1 * hfx;
-    e = hxs * ((r1 - t) / (6.0f - x * t));
-    if (k == 0) return x - (x * e - hxs);
-    e = (x * (e - c) - c);
-    e -= hxs;
-    if (k == -1) return 0.5f * (x - e) - 0.5f;
-    if (k == 1) return x < -0.25f ? -2.0f * (e - (x + 0.5f)) : one + 2.0f * (x - e);
-    if (k <= -2 || k > 56) {
-        y = one - (e - x);
-        y = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, y) + ((uint32_t)k << 23));
-        return y - one;
-    }
-    if (k < 23) {
-        t = __builtin_bit_cast(float, 0x3f800000u - (0x1000000u >> k));
-        y = t - (e - x);
-        y = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, y) + ((uint32_t)k << 23));
-    } else {
-        t = __builtin_bit_cast(float, (uint32_t)(0x7f - k) << 23);
-        y = x - (e + t);
-        y += one;
-        y = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, y) + ((uint32_t)k << 23));
-    }
-    return y;
-}
-
-__host__ __device__ inline float fb_tanhf(float x) {
-    const float one = 1.0f, two = 2.0f, tiny = 1.0e-30f;
-    float t, z;
-    const int32_t jx = __builtin_bit_cast(int32_t, x);
-    const int32_t ix = jx & 0x7fffffff;
-    if (ix >= 0x7f800000) return jx >= 0 ? one / x + one : one / x - one;
-    if (ix < 0x41b00000) {  // |x| < 22
-        if (ix == 0) return x;
-        if (ix < 0x24000000) return x * (one + x);  // |x| < 2^-55
-        if (ix >= 0x3f800000) {
-            t = fb_expm1f(two * fabsf(x));
-            z = one - two / (t + two);
-        } else {
-            t = fb_expm1f(-two * fabsf(x));
-            z = -t / (t + two);
-        }
-    } else {
-        z = one - tiny;
-    }
-    return jx >= 0 ? z : -z;
-}
-
 // tanh GELU in the reference's operation order (runtime/src/ops.rs:145-149).
 __device__ __forceinline__ float gelu(float x) {
     const float A = 0.044715f;
     const float S = 0.7978846f;
     float inner = S * x * (1.0f + A * x * x);
-    return 0.5f * x * (1.0f + fb_tanhf(inner));
+    return 0.5f * x * (1.0f + tanhf_select(inner));
 }
 
 // One block's term of the reference dot, (sumi as f32) * (d_w * d_x), each product rounded
@@ -228,14 +130,35 @@ __device__ __forceinline__ void prep_from_q8(const uint32_t *q, uint32_t *a) {
     }
 }
 
+// Cross-lane helpers; every lane of the wave must be active. DPP quad_perm [1,0,3,2] and
+// [2,3,0,1] exchange lanes j ^ 1 and j ^ 2; row_half_mirror and row_mirror pair the quads and
+// octets of a row of 16 lanes; ds_swizzle in bit-mask mode with xor 16 exchanges lanes j ^ 16
+// within each half-wave.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ uint32_t swz_xor16(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401f);
+}
+__device__ __forceinline__ float maxf_bits(float a, uint32_t b) { return fmaxf(a, __builtin_bit_cast(float, b)); }
+
+// Max over each 32-lane half-wave of non-NaN values, returned to every lane of the half.
+__device__ __forceinline__ float half_max(float m) {
+    m = maxf_bits(m, dpp<0xb1>(__builtin_bit_cast(uint32_t, m)));
+    m = maxf_bits(m, dpp<0x4e>(__builtin_bit_cast(uint32_t, m)));
+    m = maxf_bits(m, dpp<0x141>(__builtin_bit_cast(uint32_t, m)));
+    m = maxf_bits(m, dpp<0x140>(__builtin_bit_cast(uint32_t, m)));
+    return maxf_bits(m, swz_xor16(__builtin_bit_cast(uint32_t, m)));
+}
+
 // Q8_0 quantisation of one 32-value block held by a 32-lane half-wave (lane j of the half
 // holds element j), as runtime/src/ops.rs:95-105: amax fold from 0 ignoring NaN, d = amax/127,
 // id = 1/d (0 when d == 0), q = round-half-away(v * id) saturated. Returns q for this lane and
-// the f16 bits of d in *dbits (same in every lane of the half).
+// the f16 bits of d in *dbits (same in every lane of the half). The block maximum does not
+// depend on the order of the maxima (no value is NaN after fmaxf(0, |v|)).
 __device__ __forceinline__ int quant_q8_half(float v, uint16_t *dbits) {
-    float m = fmaxf(0.0f, fabsf(v));
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float m = half_max(fmaxf(0.0f, fabsf(v)));
     float d = m / 127.0f;
     float id = d != 0.0f ? 1.0f / d : 0.0f;
     *dbits = f2h_rne(d);
@@ -246,16 +169,15 @@ __device__ __forceinline__ int quant_q8_half(float v, uint16_t *dbits) {
 // store it at dst (ACT_DW dwords) when ok. Element 4d+k (k < 4) sits in byte k, low nibble, of
 // dword d; element 16+4d+k in byte k, high nibble. Every lane of the wave must call this.
 __device__ __forceinline__ void store_prep_half(int q, uint16_t dbits, int j, uint32_t *dst, bool ok) {
+    const uint32_t qp = swz_xor16((uint32_t)q);  // element j ^ 16 of the half
     const int k = j & 3;
-    const int sh = 8 * k + (j >= 16 ? 4 : 0);
-    uint32_t ch = (uint32_t)((q >> 4) & 15) << sh;
-    uint32_t cl = (uint32_t)((q & 15) ^ 8) << sh;
-    ch |= __shfl_xor(ch, 1);
-    cl |= __shfl_xor(cl, 1);
-    ch |= __shfl_xor(ch, 2);
-    cl |= __shfl_xor(cl, 2);
-    ch |= __shfl_xor(ch, 16);
-    cl |= __shfl_xor(cl, 16);
+    // lanes j < 16: byte k of dword j >> 2 from elements j (low nibble) and j + 16 (high nibble)
+    uint32_t ch = ((((uint32_t)q >> 4) & 15u) | (((qp >> 4) & 15u) << 4)) << (8 * k);
+    uint32_t cl = ((((uint32_t)q & 15u) ^ 8u) | (((qp & 15u) ^ 8u) << 4)) << (8 * k);
+    ch |= dpp<0xb1>(ch);
+    cl |= dpp<0xb1>(cl);
+    ch |= dpp<0x4e>(ch);
+    cl |= dpp<0x4e>(cl);
     if (!ok) return;
     if (j < 16 && k == 0) dst[j >> 2] = ch;
     if (j < 16 && k == 1) dst[4 + (j >> 2)] = cl;
@@ -265,12 +187,12 @@ __device__ __forceinline__ void store_prep_half(int q, uint16_t dbits, int j, ui
 
 // Workspace layout for n_tok tokens through one layer (offsets in bytes, 256-aligned).
 struct WsLayout {
-    size_t ctl;     // u32[64]: [0] router-guard fallback count
+    size_t ctl;     // u32[64]: [0] router fallback count; [16..24) decode: h row of each slot
     size_t stats;   // double2[n_tok][n_exp]: exact-sum estimate and error bound per logit
     size_t ids;     // i32[n_tok][top_k]
     size_t wts;     // f32[n_tok][top_k]
     size_t xact;    // u32[n_tok][d/32][ACT_DW]
-    size_t hact;    // u32[pairs][ff/32][ACT_DW]
+    size_t hact;    // u32[pairs + top_k][ff/32][ACT_DW]
     size_t order;   // i32[pairs]
     size_t pos_of;  // i32[pairs]
     size_t gstart;  // i32[n_exp + 1]
@@ -294,7 +216,7 @@ inline WsLayout ws_layout(const rvm_layer *L, int n_tok) {
     w.ids = take(pairs * 4);
     w.wts = take(pairs * 4);
     w.xact = take((size_t)n_tok * (L->d / QK) * ACT_DW * 4);
-    w.hact = take(pairs * (L->ff / QK) * ACT_DW * 4);
+    w.hact = take((pairs + L->top_k) * (L->ff / QK) * ACT_DW * 4);  // + decode correction rows
     w.order = take(pairs * 4);
     w.pos_of = take(pairs * 4);
     w.gstart = take((size_t)(L->n_exp + 1) * 4);
@@ -334,8 +256,9 @@ inline int with_steps(int n, F &&f) {
 int max_lds_per_block();
 
 // Kernel launchers shared across translation units.
+// k_router (logit statistics and the Q8_0 input), then k_select unless select is false.
 int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, float eps, uint8_t *ws,
-                  const WsLayout &lay, int32_t *ids, float *wts, float *logits);
+                  const WsLayout &lay, int32_t *ids, float *wts, float *logits, bool select);
 int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart);
 
 }  // namespace rvm
