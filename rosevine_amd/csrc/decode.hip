@@ -134,9 +134,9 @@ __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
     st.load(xact, S * 3);  // in flight during the selection
     if (blockIdx.x > 0) {
         const int b = blockIdx.x - 1, slot = b / T, t = b - slot * T;
-        select_token<PER, GU_WAVES>(u.sel, stats, bias, W, x, n_exp, top_k, pre_norm, eps, exact, false, false, ctl,
-                                    nullptr);
-        const int e = __builtin_amdgcn_readfirstlane(clamp_expert(u.sel.spec[slot], n_exp));
+        select_token<PER, GU_WAVES, false>(u.sel, stats, bias, W, x, n_exp, top_k, pre_norm, eps, exact, false, false,
+                                           ctl, nullptr);
+        const int e = __builtin_amdgcn_readfirstlane(clamp_expert(spec_id(u.sel, slot, top_k), n_exp));
         gateup_tile<PER, true>(nib, scl, e, t, T, st, act, u.terms, hact + ((size_t)slot * T + t) * ACT_DW);
         return;
     }

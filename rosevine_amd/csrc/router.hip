@@ -16,12 +16,12 @@
 
 namespace rvm {
 
-constexpr int RWAVES = 4;    // waves (experts) per router workgroup
+constexpr int RWAVES = 1;  // waves (experts) per router workgroup: one expert per CU spreads the row loads
 constexpr int SEL_WAVES = 8;  // waves of the selecting workgroup
 
 // F4 = d / 256: lane l owns elements [4*F4*l, 4*F4*(l+1)) of a router row.
 template <int F4>
-__global__ __launch_bounds__(256) void k_router(const float *__restrict__ W, const float *__restrict__ x, int n_exp,
+__global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict__ W, const float *__restrict__ x, int n_exp,
                                                 int pre_norm, float eps, double2 *__restrict__ stats,
                                                 uint32_t *__restrict__ xact) {
     constexpr int d = 256 * F4, C = 4 * F4, nb = d / QK;
@@ -44,6 +44,18 @@ __global__ __launch_bounds__(256) void k_router(const float *__restrict__ W, con
     const float qv0 = hb0 < nb ? xt[hb0 * QK + j] : 0.0f;
     float4 xv[F4];
     const float scale = load_x_chunk<F4>(xt, lane, pre_norm, eps, xv);
+
+    // Q8_0 quantisation of the layer input, one 32-block per half-wave (runtime/src/ops.rs:95-105),
+    // while the row loads are in flight.
+    for (int base = base0; base < nb; base += hw_total) {
+        const int hb = base + (lane >> 5);
+        const bool ok = hb < nb;
+        float v = base == base0 ? qv0 : (ok ? xt[hb * QK + j] : 0.0f);
+        if (pre_norm) v = v * scale;
+        uint16_t dbits;
+        const int q = quant_q8_half(v, &dbits);
+        store_prep_half(q, dbits, j, xact + ((size_t)tok * nb + (ok ? hb : 0)) * ACT_DW, ok);
+    }
 
     if (have) {
         float p[C];
@@ -78,17 +90,6 @@ __global__ __launch_bounds__(256) void k_router(const float *__restrict__ W, con
             const double bound = babs * g / (1.0 - (double)d * g) * (1.0 + 0x1p-20) + 1e-300;
             stats[(size_t)tok * n_exp + e] = make_double2(total, bound);
         }
-    }
-
-    // Q8_0 quantisation of the layer input, one 32-block per half-wave (runtime/src/ops.rs:95-105).
-    for (int base = base0; base < nb; base += hw_total) {
-        const int hb = base + (lane >> 5);
-        const bool ok = hb < nb;
-        float v = base == base0 ? qv0 : (ok ? xt[hb * QK + j] : 0.0f);
-        if (pre_norm) v = v * scale;
-        uint16_t dbits;
-        const int q = quant_q8_half(v, &dbits);
-        store_prep_half(q, dbits, j, xact + ((size_t)tok * nb + (ok ? hb : 0)) * ACT_DW, ok);
     }
 }
 
@@ -184,7 +185,7 @@ int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, floa
     const int pre = (flags & RVM_PRE_NORM) ? 1 : 0;
     return with_steps(L->d / 256, [&](auto f4) {
         constexpr int F4 = decltype(f4)::value;
-        hipLaunchKernelGGL(k_router<F4>, dim3(groups, n_tok), dim3(256), 0, cur_stream(), L->router, x, L->n_exp,
+        hipLaunchKernelGGL(k_router<F4>, dim3(groups, n_tok), dim3(RWAVES * 64), 0, cur_stream(), L->router, x, L->n_exp,
                            pre, eps, (double2 *)(ws + lay.stats), (uint32_t *)(ws + lay.xact));
         int rc = launched();
         if (rc || !select) return rc;

@@ -262,7 +262,9 @@ __device__ void exact_all(SelShared<F4, NW> &sh, const float *__restrict__ W, co
 // ids in sh.sel and its weights in sh.wsel (sh.spec keeps the S-ranking ids); without it only
 // sh.spec is meaningful. With publish set, the logits go to lg_t (when not null) and a fallback
 // is counted in ctl[0].
-template <int F4, int NW>
+// With CERTIFY false only the S ranking runs (no certificate, no exact path): sh.sel and sh.hits
+// are set, and spec_id gives the ids every workgroup agrees on.
+template <int F4, int NW, bool CERTIFY = true>
 __device__ void select_token(SelShared<F4, NW> &sh, const double2 *__restrict__ st, const float *__restrict__ bias,
                              const float *__restrict__ W, const float *__restrict__ xt, int n_exp, int top_k,
                              int pre_norm, float eps, int exact, bool publish, bool exact_here,
@@ -317,6 +319,14 @@ __device__ void select_token(SelShared<F4, NW> &sh, const double2 *__restrict__ 
         r += (int)dpp<0xb1>((uint32_t)r);
         if (tpe == 4) r += (int)dpp<0x4e>((uint32_t)r);
         const bool own = part == 0 && e < n_exp;
+        if (!CERTIFY) {
+            if (own && r < top_k) {
+                atomicAdd(&sh.hits[r], 1);
+                sh.sel[r] = e;
+            }
+            __syncthreads();
+            return;
+        }
         uint32_t uk = 0;  // the highest upper bound among unselected experts, rounded up to f32
         bool bad = false;
         if (own) {
@@ -381,7 +391,7 @@ __device__ void select_token(SelShared<F4, NW> &sh, const double2 *__restrict__ 
         // can differ between workgroups, so every workgroup then uses experts 0.. instead.
         bool ties = false;
         for (int j = 0; j < top_k; ++j) ties |= sh.hits[j] != 1;
-        if (lane < top_k) sh.spec[lane] = ties ? lane : sh.sel[lane];
+        if (lane < top_k) sh.spec[lane] = ties ? lane : sh.sel[lane];  // = spec_id
     }
     __syncthreads();
     if (!sh.pass && exact_here) {
@@ -435,6 +445,15 @@ __device__ void select_token(SelShared<F4, NW> &sh, const double2 *__restrict__ 
         }
     }
     __syncthreads();
+}
+
+// The S-ranking id of slot j as every workgroup computes it (experts 0.. under tied keys); valid
+// after select_token in either mode.
+template <int F4, int NW>
+__device__ __forceinline__ int spec_id(const SelShared<F4, NW> &sh, int j, int top_k) {
+    bool ties = false;
+    for (int i = 0; i < top_k; ++i) ties |= sh.hits[i] != 1;
+    return ties ? j : sh.sel[j];
 }
 
 // The renormalised weights of a certified selection (sh.pass), from the estimates rounded to
