@@ -67,16 +67,22 @@ union GateUpShared {
     float terms[PER * GU_WAVES][64];
 };
 
-// One 64-row tile t of expert e: every wave loads its PER steps (16-byte nibble entries and the
-// scales), the activation blocks are stored to LDS from st (when STAGE) behind the loads, each
-// lane forms its block terms, and wave 0 folds each row's terms in block order (the reference's
-// sequential fold, expert_kernel.rs:148-159), pairs gate row l with up row l + 32, applies GeGLU
-// and writes the Q8_0 block of the tile's 32 h values to hdst. Called by every thread.
+// One 64-row tile t of expert e, and the down terms of the h block it produces.
+//   gate/up: every wave loads its PER steps (16-byte nibble entries and the scales), the activation
+//   blocks are stored to LDS from st (when STAGE) behind the loads, each lane forms its block
+//   terms, and wave 0 folds each row's terms in block order (the reference's sequential fold,
+//   expert_kernel.rs:148-159), pairs gate row l with up row l + 32, applies GeGLU and writes the
+//   Q8_0 block t of h (32 values) to hdst and to LDS.
+//   down: h block t meets block t of every down row r of the same expert: thread i forms the terms
+//   (sumi as f32) * (d_w * d_h) of rows i, i + 512, ... (their entries are loaded with the gate/up
+//   ones) and writes them to dterm[r]; the down kernel folds each row's T terms in block order.
+// Called by every thread.
 template <int PER, bool STAGE, class St>
-__device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl, int e,
-                                            int t, int T, const St &st, uint4 *act, float (*terms)[64],
-                                            uint32_t *__restrict__ hdst) {
-    constexpr int S = PER * GU_WAVES;
+__device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl,
+                                            const uint4 *__restrict__ dnib, const uint16_t *__restrict__ dscl,
+                                            int e, int t, int T, const St &st, uint4 *act, float (*terms)[64],
+                                            uint32_t *hprep, uint32_t *__restrict__ hdst, float *__restrict__ dterm) {
+    constexpr int S = PER * GU_WAVES, d = 256 * PER, RD = (d + GU_WAVES * 64 - 1) / (GU_WAVES * 64);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const size_t base = (((size_t)e * T + t) * S + (size_t)w * PER) * 64 + lane;
@@ -87,9 +93,21 @@ __device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const
         wv[i] = nib[base + (size_t)i * 64];
         sv[i] = scl[base + (size_t)i * 64];
     }
+    // down entries of block t: RVM_PACK_ROWS32 with Sd = T / 2 steps; row r is lane
+    // (r & 31) + 32 * (t / Sd) of tile r / 32 at step t % Sd
+    const int Sd = T >> 1, half = t >= Sd ? 1 : 0, sd = t - half * Sd, Td = d / 32;
+    uint4 dv[RD];
+    uint32_t ds[RD];
+#pragma unroll
+    for (int i = 0; i < RD; ++i) {
+        const int r = min((int)threadIdx.x + i * GU_WAVES * 64, d - 1);
+        const size_t ent = (((size_t)e * Td + (r >> 5)) * Sd + sd) * 64 + 32 * half + (r & 31);
+        dv[i] = dnib[ent];
+        ds[i] = dscl[ent];
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (STAGE) st.store(act);
-    __syncthreads();  // act is staged; and the previous user of terms is done
+    __syncthreads();  // act is staged; and the previous user of terms and hprep is done
     float tv[PER];
     lane_terms<PER>(wv, sv, act + w * PER * 3, tv);
 #pragma unroll
@@ -107,6 +125,20 @@ __device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const
         uint16_t dbits;
         const int q = quant_q8_half(h, &dbits);
         store_prep_half(q, dbits, lane & 31, hdst, lane < 32);
+        store_prep_half(q, dbits, lane & 31, hprep, lane < 32);
+    }
+    __syncthreads();
+    {
+        const uint4 *hp = (const uint4 *)hprep;
+        const uint4 a0 = hp[0], a1 = hp[1];
+        const float dx = __builtin_bit_cast(float, hp[2].x);
+        const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+        for (int i = 0; i < RD; ++i) {
+            const int r = (int)threadIdx.x + i * GU_WAVES * 64;
+            const float term = block_term(block_dot(dv[i], a), h2f((uint16_t)ds[i]), dx);
+            if (r < d) dterm[r] = term;
+        }
     }
 }
 
@@ -119,14 +151,16 @@ __device__ __forceinline__ int clamp_expert(int e, int n_exp) { return (unsigned
 // tile (b % T) of the S ranking's experts.
 template <int PER>  // steps per wave = (d / 32) / GU_WAVES = d / 256
 __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
-    const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl, const double2 *__restrict__ stats,
-    const float *__restrict__ bias, const float *__restrict__ W, const float *__restrict__ x, int n_exp, int top_k,
-    int pre_norm, float eps, int exact, uint32_t *__restrict__ ctl, int32_t *__restrict__ ids,
-    float *__restrict__ wts, const uint4 *__restrict__ xact, uint32_t *__restrict__ hact, int T) {
-    constexpr int S = PER * GU_WAVES;
+    const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl, const uint4 *__restrict__ dnib,
+    const uint16_t *__restrict__ dscl, const double2 *__restrict__ stats, const float *__restrict__ bias,
+    const float *__restrict__ W, const float *__restrict__ x, int n_exp, int top_k, int pre_norm, float eps, int exact,
+    uint32_t *__restrict__ ctl, int32_t *__restrict__ ids, float *__restrict__ wts, const uint4 *__restrict__ xact,
+    uint32_t *__restrict__ hact, float *__restrict__ dterm, int T) {
+    constexpr int S = PER * GU_WAVES, d = 256 * PER;
     using St = Stage<S * 3, GU_WAVES * 64>;
     __shared__ uint4 act[St::SLOTS];
     __shared__ GateUpShared<PER> u;
+    __shared__ uint4 hprep[3];
     __shared__ int fix_e[MAX_TOPK];
     __shared__ int n_fix;
     const int lane = threadIdx.x & 63;
@@ -137,7 +171,8 @@ __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
         select_token<PER, GU_WAVES, false>(u.sel, stats, bias, W, x, n_exp, top_k, pre_norm, eps, exact, false, false,
                                            ctl, nullptr);
         const int e = __builtin_amdgcn_readfirstlane(clamp_expert(spec_id(u.sel, slot, top_k), n_exp));
-        gateup_tile<PER, true>(nib, scl, e, t, T, st, act, u.terms, hact + ((size_t)slot * T + t) * ACT_DW);
+        gateup_tile<PER, true>(nib, scl, dnib, dscl, e, t, T, st, act, u.terms, (uint32_t *)hprep,
+                               hact + ((size_t)slot * T + t) * ACT_DW, dterm + ((size_t)slot * T + t) * d);
         return;
     }
     select_token<PER, GU_WAVES>(u.sel, stats, bias, W, x, n_exp, top_k, pre_norm, eps, exact, true, true, ctl,
@@ -165,96 +200,59 @@ __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
     // selection changed the set of experts)
     for (int m = 0; m < n_fix; ++m)
         for (int t = 0; t < T; ++t) {
+            const size_t row = (size_t)(top_k + m) * T + t;
             if (m == 0 && t == 0)
-                gateup_tile<PER, true>(nib, scl, fix_e[m], t, T, st, act, u.terms,
-                                       hact + ((size_t)(top_k + m) * T + t) * ACT_DW);
+                gateup_tile<PER, true>(nib, scl, dnib, dscl, fix_e[m], t, T, st, act, u.terms, (uint32_t *)hprep,
+                                       hact + row * ACT_DW, dterm + row * d);
             else
-                gateup_tile<PER, false>(nib, scl, fix_e[m], t, T, st, act, u.terms,
-                                        hact + ((size_t)(top_k + m) * T + t) * ACT_DW);
+                gateup_tile<PER, false>(nib, scl, dnib, dscl, fix_e[m], t, T, st, act, u.terms, (uint32_t *)hprep,
+                                        hact + row * ACT_DW, dterm + row * d);
         }
 }
 
-template <int S>  // steps per lane = ff / 64
-__global__ __launch_bounds__(MAX_TOPK * 64) void k_down_decode(const uint4 *__restrict__ nib,
-                                                               const uint16_t *__restrict__ scl,
-                                                               const int32_t *__restrict__ ids,
-                                                               const float *__restrict__ wts,
-                                                               const int32_t *__restrict__ hslot,
-                                                               const float *__restrict__ dscale,
-                                                               const uint4 *__restrict__ hact,
-                                                               float *__restrict__ out, int T, int top_k) {
-    constexpr int NB = 2 * S;  // h blocks per slot
-    constexpr int IT = (MAX_TOPK * NB * 3 + MAX_TOPK * 64 - 1) / (MAX_TOPK * 64);
-    __shared__ uint4 act[IT * MAX_TOPK * 64];
-    __shared__ float half2[MAX_TOPK][S][32];  // the second half's block terms of each row
+// Down and combine: thread (slot k, row) folds the T = 2S down terms of its row in block order
+// (dot_q8_scalar's sequential fold from 0.0), then the first 32 threads combine (y * ds) * w in
+// slot order, the first term assigned (runtime/src/exec.rs:626-638). The terms of selected slot k
+// sit in the h row hslot[k]; that is k unless the exact selection changed the experts, so the
+// terms are read for k first and again only when the map differs. Every global load is issued
+// before the first use.
+template <int S>  // ff / 64
+__global__ __launch_bounds__(256) void k_down_fold(const float *__restrict__ dterm, const int32_t *__restrict__ ids,
+                                                   const float *__restrict__ wts, const int32_t *__restrict__ hslot,
+                                                   const float *__restrict__ dscale, float *__restrict__ out, int d,
+                                                   int top_k) {
+    constexpr int T = 2 * S;
     __shared__ float ys[MAX_TOPK][32];
-    __shared__ float coef[2][MAX_TOPK];
-    const int t = blockIdx.x;
-    const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    // Waves past top_k load slot 0's tile too (unused) so that the loads need no branch.
-    const int e = ids[j < top_k ? j : 0];
+    __shared__ float coef[2][MAX_TOPK];  // ds and w of each slot
+    const int row = blockIdx.x * 32 + (threadIdx.x & 31);
+    const int k = threadIdx.x >> 5;  // slot
+    const int kc = min(k, top_k - 1);
+    float v[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) v[t] = dterm[((size_t)kc * T + t) * d + row];
     if (threadIdx.x < (unsigned)top_k) {
         coef[0][threadIdx.x] = dscale ? dscale[ids[threadIdx.x]] : 1.0f;
         coef[1][threadIdx.x] = wts[threadIdx.x];
     }
-    // slot k's h blocks are the hslot[k]-th row of blocks of hact (gathered; indices clamped so
-    // that the loads need no branch)
-    uint4 av[IT];
+    bool moved = false;
+    for (int j = 0; j < top_k; ++j) moved |= hslot[j] != j;
+    if (moved) {
+        const int hr = min((unsigned)hslot[kc], (unsigned)(2 * top_k - 1));
 #pragma unroll
-    for (int i = 0; i < IT; ++i) {
-        const int idx = min((int)threadIdx.x + i * MAX_TOPK * 64, top_k * NB * 3 - 1);
-        const int k = idx / (NB * 3);
-        const int row = min((unsigned)hslot[k], (unsigned)(2 * top_k - 1));
-        av[i] = hact[(size_t)row * NB * 3 + (idx - k * NB * 3)];
+        for (int t = 0; t < T; ++t) v[t] = dterm[((size_t)hr * T + t) * d + row];
     }
-    __builtin_amdgcn_sched_barrier(0);  // activation loads first: the memory counter drains in order
-    const size_t base = ((size_t)e * T + t) * S * 64 + lane;
-    uint4 wv[S];
-    uint32_t sv[S];
+    float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < S; ++i) {
-        wv[i] = nib[base + (size_t)i * 64];
-        sv[i] = scl[base + (size_t)i * 64];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < IT; ++i) act[threadIdx.x + i * MAX_TOPK * 64] = av[i];
-    __syncthreads();
-    {
-        // computed by every wave (those past top_k on slot 0's data) so that the weight loads stay
-        // ahead of the barrier instead of sinking into a branch
-        const int kp = lane >> 5;
-        float tv[S];
-        lane_terms<S>(wv, sv, act + ((j < top_k ? j : 0) * NB + kp * S) * 3, tv);
-        // sequential fold in block order: lanes < 32 hold blocks 0..S-1 of row `lane`, lanes
-        // + 32 blocks S..2S-1 of the same row, passed through LDS
-        if (lane >= 32) {
-#pragma unroll
-            for (int i = 0; i < S; ++i) half2[j][i][lane - 32] = tv[i];
-        }
-        wave_lds_sync();
-        if (lane < 32) {
-            float hv[S];
-#pragma unroll
-            for (int i = 0; i < S; ++i) hv[i] = half2[j][i][lane];
-            float acc = 0.0f;
-#pragma unroll
-            for (int i = 0; i < S; ++i) acc = acc + tv[i];
-#pragma unroll
-            for (int i = 0; i < S; ++i) acc = acc + hv[i];
-            if (j < top_k) ys[j][lane] = acc;
-        }
-    }
+    for (int t = 0; t < T; ++t) acc = acc + v[t];
+    if (k < top_k) ys[k][threadIdx.x & 31] = acc;
     __syncthreads();
     if (threadIdx.x < 32) {
-        // (y * ds) * w in slot order, the first term assigned (runtime/src/exec.rs:626-638)
         float o = 0.0f;
-        for (int jj = 0; jj < top_k; ++jj) {
-            const float v = ys[jj][threadIdx.x] * coef[0][jj] * coef[1][jj];
-            o = jj == 0 ? v : o + v;
+        for (int j = 0; j < top_k; ++j) {
+            const float cj = ys[j][threadIdx.x] * coef[0][j] * coef[1][j];
+            o = j == 0 ? cj : o + cj;
         }
-        out[(size_t)t * 32 + threadIdx.x] = o;
+        out[row] = o;
     }
 }
 
@@ -277,24 +275,22 @@ extern "C" int rvm_moe_decode(const rvm_layer *L, const float *x, float *out, in
     const size_t gu_entries = (size_t)L->n_exp * 2 * L->ff * (L->d / QK);
     const uint4 *gnib = (const uint4 *)L->gate_up;
     const uint16_t *gscl = (const uint16_t *)((const uint8_t *)L->gate_up + gu_entries * 16);
-    const int pre = (flags & RVM_PRE_NORM) ? 1 : 0, exact = (flags & RVM_EXACT_SELECT) ? 1 : 0;
-    rc = with_steps(L->d / 256, [&](auto per) {
-        hipLaunchKernelGGL(k_gateup_decode<decltype(per)::value>, dim3(1 + L->top_k * Tg), dim3(GU_WAVES * 64), 0,
-                           cur_stream(), gnib, gscl, (const double2 *)(w + lay.stats), L->router_bias, L->router, x,
-                           L->n_exp, L->top_k, pre, eps, exact, (uint32_t *)(w + lay.ctl), ids, wts,
-                           (const uint4 *)(w + lay.xact), (uint32_t *)(w + lay.hact), Tg);
-        return launched();
-    });
-    if (rc) return rc;
-
-    const int Td = L->d / 32;
     const size_t dn_entries = (size_t)L->n_exp * L->d * (L->ff / QK);
     const uint4 *dnib = (const uint4 *)L->down;
     const uint16_t *dscl = (const uint16_t *)((const uint8_t *)L->down + dn_entries * 16);
+    const int pre = (flags & RVM_PRE_NORM) ? 1 : 0, exact = (flags & RVM_EXACT_SELECT) ? 1 : 0;
+    rc = with_steps(L->d / 256, [&](auto per) {
+        hipLaunchKernelGGL(k_gateup_decode<decltype(per)::value>, dim3(1 + L->top_k * Tg), dim3(GU_WAVES * 64), 0,
+                           cur_stream(), gnib, gscl, dnib, dscl, (const double2 *)(w + lay.stats), L->router_bias,
+                           L->router, x, L->n_exp, L->top_k, pre, eps, exact, (uint32_t *)(w + lay.ctl), ids, wts,
+                           (const uint4 *)(w + lay.xact), (uint32_t *)(w + lay.hact), (float *)(w + lay.dterm), Tg);
+        return launched();
+    });
+    if (rc) return rc;
     return with_steps(L->ff / 64, [&](auto s) {
-        hipLaunchKernelGGL(k_down_decode<decltype(s)::value>, dim3(Td), dim3(MAX_TOPK * 64), 0, cur_stream(), dnib,
-                           dscl, ids, wts, (const int32_t *)(w + lay.ctl) + 16, L->down_scale,
-                           (const uint4 *)(w + lay.hact), out, Td, L->top_k);
+        hipLaunchKernelGGL(k_down_fold<decltype(s)::value>, dim3(L->d / 32), dim3(256), 0, cur_stream(),
+                           (const float *)(w + lay.dterm), ids, wts, (const int32_t *)(w + lay.ctl) + 16,
+                           L->down_scale, out, L->d, L->top_k);
         return launched();
     });
 }

@@ -196,7 +196,8 @@ struct WsLayout {
     size_t order;   // i32[pairs]
     size_t pos_of;  // i32[pairs]
     size_t gstart;  // i32[n_exp + 1]
-    size_t y;       // f32[pairs][d]
+    size_t y;       // f32[pairs][d] (batched path)
+    size_t dterm;   // f32[2 top_k][ff/32][d] (decode: down terms per slot and h block)
     size_t total;
 };
 
@@ -221,6 +222,8 @@ inline WsLayout ws_layout(const rvm_layer *L, int n_tok) {
     w.pos_of = take(pairs * 4);
     w.gstart = take((size_t)(L->n_exp + 1) * 4);
     w.y = n_tok > 1 ? take(pairs * L->d * 4) : take(0);
+    // kept for every n_tok so that a workspace sized for a batch also serves rvm_moe_decode
+    w.dterm = take((size_t)2 * L->top_k * (L->ff / QK) * L->d * 4);
     w.total = o;
     return w;
 }
