@@ -30,6 +30,9 @@ METRIC = "MoE-layer decode tokens/s + achieved HBM GB/s (% of peak), batch 1"
 HBM_PEAK_GBS = 8000.0
 EXPERT_BYTES = 2816 // 32 * 18 * 1408 + 704 // 32 * 18 * 2816  # 3,345,408
 ROUTER_BYTES = 128 * 2816 * 4  # 1,441,792
+# HBM bytes one decode call moves (read + written), from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
+# this workload calibrated against a device copy of known size (profiles/decode_hbm_traffic.md).
+MEASURED_TRAFFIC = 33_696_704
 
 
 def log(msg: str) -> None:
@@ -76,6 +79,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="only copy this many bytes device-to-device 5 times (the calibration of the HBM "
+                         "byte counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the MoE path runs on one "
@@ -87,6 +93,13 @@ def main() -> int:
     from rosevine_amd import hip, moe, synth
 
     hip.init(0)
+    if args.copy_bytes:
+        a, b = hip.DevBuf(args.copy_bytes), hip.DevBuf(args.copy_bytes)
+        for _ in range(5):
+            hip.copy(b, a, args.copy_bytes)
+        hip.sync()
+        log(f"[bench] copied {args.copy_bytes} bytes 5 times")
+        return 0
     K, W = args.steps, args.warmup
     log(f"[bench] layer 128x(1408x2816 + 2816x704) Q4_0, tokens {W}+{K}")
     router = synth.router_weights(args.seed, 0)
@@ -165,9 +178,9 @@ def main() -> int:
         "config": {"workload": "single MoE layer, batch-1 decode, 10k back-to-back tokens, iid routing",
                    "n_exp": synth.N_EXP, "top_k": synth.TOP_K, "d": synth.D, "ff": synth.FF,
                    "tokens": K, "graph_tokens": ch, "router_fallbacks": fallbacks},
-        "roofline": {"bound": "hbm", "kernel": "rvm_moe_decode (k_router + k_gateup_decode + k_down_decode)",
+        "roofline": {"bound": "hbm", "kernel": "rvm_moe_decode (k_router + k_gateup_decode + k_down_fold)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC,
                      "bytes_per_launch": bytes_tok},
         "cpu_baseline": cpu,
     }

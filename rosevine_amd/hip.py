@@ -131,6 +131,11 @@ def init(device: int = 0) -> None:
     check(lib().rvh_init(device))
 
 
+def copy(dst: DevBuf, src: DevBuf, nbytes: int, dst_off: int = 0, src_off: int = 0) -> None:
+    """rvh_copy: device-to-device, ordered on the current stream."""
+    check(lib().rvh_copy(_need(dst, nbytes, dst_off), _need(src, nbytes, src_off), nbytes))
+
+
 def sync() -> None:
     check(lib().rvh_sync())
 
