@@ -70,6 +70,112 @@ def cpu_baseline(seed: int, n_tokens: int, seconds: float, threads: int):
                       f"({'avx2_q8' if orc.CpuBaseline.uses_avx2() else 'scalar'} kernel, {threads} threads)"}
 
 
+def _timed(run, iters: int, warm: int):
+    """Mean ms of run() over iters calls after warm calls, timed with events on the current stream."""
+    from rosevine_amd import hip
+    for _ in range(warm):
+        run()
+    hip.sync()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record()
+    for _ in range(iters):
+        run()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_ms(e1) / iters
+
+
+def other_workload(args) -> int:
+    """The other configurations of the decode/prefill path, one JSON line each (not the headline)."""
+    import numpy as np
+
+    from rosevine_amd import hip, moe, synth
+
+    E, K8, D, FF = synth.N_EXP, synth.TOP_K, synth.D, synth.FF
+    ops_pair = 2 * (2 * FF * D + D * FF)  # int8 multiply-adds x 2 per token-expert pair
+    stream = hip.Stream()
+    stream.use()
+    line = {"n_gpus": 1, "higher_is_better": True, "vs_baseline": None, "dtype": "int4xint8->int32, f32",
+            "data": "synthetic (seeded Q4_0 experts, N(0,1) tokens, N(0,0.02) router)"}
+    if args.workload in ("prefill512", "ragged32"):
+        n = 512 if args.workload == "prefill512" else 32
+        bias = None if n == 512 else synth.zipf_bias(args.seed)
+        layer = moe.MoeLayer(E, K8, D, FF, synth.router_weights(args.seed, 0), bias)
+        layer.synth_weights(args.seed, synth.gate_up_stream(0), synth.down_stream(0))
+        xs = [hip.DevBuf.from_array(synth.tokens(args.seed + 200 + i, n)) for i in range(4)]
+        out = hip.DevBuf(n * D * 4)
+        ws = moe.Workspace(layer, n)
+        it = [0]
+
+        def run():
+            moe.forward(layer, xs[it[0] % 4], out, n, ws)
+            it[0] += 1
+
+        ms = _timed(run, max(5, args.steps // (100 if n == 512 else 10)), 3)
+        moe.forward(layer, xs[0], out, n, ws)
+        ids, _ = ws.selection(layer, n)
+        distinct = len(set(int(v) for v in ids.reshape(-1)))
+        nbytes = distinct * EXPERT_BYTES + ROUTER_BYTES
+        ops = n * K8 * ops_pair
+        line.update({"metric": f"MoE-layer forward tokens/s, {n} tokens", "value": round(n / (ms / 1e3), 1),
+                     "unit": "tokens/s", "steps": max(5, args.steps // (100 if n == 512 else 10)), "warmup": 3,
+                     "ms_per_step": round(ms, 6), "scaling": "weak",
+                     "config": {"workload": args.workload, "tokens": n, "distinct_experts": distinct,
+                                "routing": "iid" if bias is None else "Zipf(1.1) router bias"},
+                     "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms / 1e3) / 1e9, 1),
+                                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                                  "bytes_per_step": nbytes, "int8_tops": round(ops / (ms / 1e3) / 1e12, 2),
+                                  "int8_frac_of_5000_tops": round(ops / (ms / 1e3) / 5.0e15, 5)}})
+    else:  # stack30
+        L = 30
+        layers = []
+        for l in range(L):
+            ly = moe.MoeLayer(E, K8, D, FF, synth.router_weights(args.seed, l), synth.router_bias(args.seed, l))
+            ly.synth_weights(args.seed, synth.gate_up_stream(l), synth.down_stream(l))
+            layers.append(ly)
+        hip.sync()
+        ws = moe.Workspace(layers[0], 1)
+        n_tok = 40
+        x = hip.DevBuf.from_array(synth.tokens(args.seed + 300, n_tok))
+        bufs = [hip.DevBuf(D * 4) for _ in range(2)]
+        nb = D * 4
+
+        def capture(t0: int, n: int) -> hip.Graph:
+            hip.Graph.begin()
+            for t in range(t0, t0 + n):
+                moe.decode(layers[0], x, bufs[0], ws, x_off=t * nb)
+                for l in range(1, L):  # the next layer's input is rms_norm(previous output, eps 1e-6)
+                    moe.decode(layers[l], bufs[(l - 1) % 2], bufs[l % 2], ws, flags=hip.PRE_NORM)
+            return hip.Graph.end()
+
+        warm, timed = capture(0, 4), capture(4, n_tok - 4)
+        warm.launch()
+        hip.sync()
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record()
+        timed.launch()
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / (n_tok - 4)
+        warm.close()
+        timed.close()
+        nbytes = L * (K8 * EXPERT_BYTES + ROUTER_BYTES)
+        line.update({"metric": "30-layer MoE stack decode tokens/s, batch 1", "value": round(1e3 / ms, 1),
+                     "unit": "tokens/s", "steps": n_tok - 4, "warmup": 4, "ms_per_step": round(ms, 6),
+                     "scaling": "weak",
+                     "config": {"workload": "stack30", "layers": L, "resident_bytes": L * layers[0].weight_bytes,
+                                "routing": "per-expert bias N(0,1)", "norm": "RMSNorm eps 1e-6 between layers"},
+                     "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms / 1e3) / 1e9, 1),
+                                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                                  "bytes_per_step": nbytes}})
+    hip.Stream.use_default()
+    stream.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -79,13 +185,17 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--workload", default="decode", choices=["decode", "prefill512", "ragged32", "stack30"],
+                    help="decode (default, the headline line); prefill512: one layer over 512 tokens; ragged32: "
+                         "one step of 32 concurrent sequences with Zipf(1.1) popularity; stack30: single-token "
+                         "decode through 30 layers with router bias and RMSNorm between layers")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only copy this many bytes device-to-device 5 times (the calibration of the HBM "
                          "byte counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the MoE path runs on one "
-              "MI355X; see the sharding notes in DESIGN.md)", file=sys.stderr)
+              "MI355X per process; experts would shard across GPUs with one all-to-all each way)", file=sys.stderr)
         return 2
 
     import numpy as np
@@ -100,6 +210,8 @@ def main() -> int:
         hip.sync()
         log(f"[bench] copied {args.copy_bytes} bytes 5 times")
         return 0
+    if args.workload != "decode":
+        return other_workload(args)
     K, W = args.steps, args.warmup
     log(f"[bench] layer 128x(1408x2816 + 2816x704) Q4_0, tokens {W}+{K}")
     router = synth.router_weights(args.seed, 0)
