@@ -1,151 +1,195 @@
-// grouped.hip - n_tok tokens through one MoE layer with device-side grouping
-// (runtime/src/exec.rs:456-475 and 540-640; the reference's host dispatch is
+// grouped.hip - n_tok tokens through one MoE layer with device-side grouping (ragged decode
+// batches and prefill; runtime/src/exec.rs:456-475 and 540-640, the reference's host dispatch is
 // runtime/src/hip_exec.rs:822-843).
 //
-//   router (router.hip)       -> ids, weights, Q8_0 activation blocks per token
-//   k_plan (router.hip)       -> pairs stably grouped by expert: order, pos_of, group starts
-//   k_gateup_grouped          -> per (expert, 64-row tile): the tile's weights are loaded into
-//                                registers once and applied to every token of the group, TB at a
-//                                time; sequential block fold, GeGLU + Q8_0 epilogue per token
-//   k_down_grouped            -> per (expert, four 32-row tiles): y rows of every pair of the group
-//   k_combine_pairs           -> out[t] = sum_j (y[pos_of[t*k+j]] * scale) * weight, slot order
-// Each token's arithmetic is the decode kernels' (same split of K, same order), so a token's
-// result does not depend on the batch it arrives in.
+//   router (router.hip)   -> ids, weights, plain Q8_0 activation rows per token
+//   k_plan (router.hip)   -> pairs stably grouped by expert, and the groups cut into 16-pair tiles
+//   k_gateup_mfma         -> per (tile, 4 row tiles of 32 gate + 32 up rows): int8 MFMA
+//                            (v_mfma_i32_16x16x32_i8, one 32-weight block per instruction) gives
+//                            each block's exact int32 sum for 16 pairs x 16 rows; the f32 terms
+//                            (sumi as f32) * (d_w * d_x) are folded in block order per output, as
+//                            dot_q8_scalar does; GeGLU and the Q8_0 of h per pair finish the tile
+//   k_down_mfma           -> per (tile, 4 row tiles of 32 down rows): the same on h, into y rows
+//   k_combine_pairs       -> out[t] = sum_j (y[pos_of[t*k+j]] * scale) * weight, slot order
+// Each output is the reference's sequential fold of exact block sums, so a token's result does not
+// depend on the batch it arrives in and equals the decode path's.
 #include "internal.hpp"
 
 namespace rvm {
 
-constexpr int G_WAVES = 8;  // K split of a gate_up tile (as k_gateup_decode)
-constexpr int TB = 4;       // tokens per pass
+typedef int v4i __attribute__((ext_vector_type(4)));
 
-// Staging of n uint4 from global to LDS in two steps, so that a kernel can issue these loads
-// before its weight loads (the memory counter drains in order) and store them after: the source
-// index is clamped so that the loads need no branch.
-template <int MAXN, int NT>
-struct StageG {
-    static constexpr int IT = (MAXN + NT - 1) / NT;
-    static constexpr int SLOTS = IT * NT;  // LDS uint4 the destination must provide
-    uint4 v[IT];
-    __device__ __forceinline__ void load(const uint4 *__restrict__ src, int n) {
-#pragma unroll
-        for (int i = 0; i < IT; ++i) v[i] = src[min((int)threadIdx.x + i * NT, n - 1)];
-    }
-    // Unconditional: entries past n repeat the last one, so the loads never sink into a branch.
-    __device__ __forceinline__ void store(uint4 *dst) const {
-#pragma unroll
-        for (int i = 0; i < IT; ++i) dst[threadIdx.x + i * NT] = v[i];
-    }
-};
+constexpr int MW = 4;  // waves (row tiles) per workgroup
 
-template <int PER>
-__device__ __forceinline__ void lane_terms_g(const uint4 (&wv)[PER], const uint32_t (&sv)[PER], const uint4 *act,
-                                             float (&t)[PER]) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const uint4 a0 = act[i * 3], a1 = act[i * 3 + 1];
-        const float dx = __builtin_bit_cast(float, act[i * 3 + 2].x);
-        const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-        t[i] = block_term(block_dot(wv[i], a), h2f((uint16_t)sv[i]), dx);
+// 8 int8 weights of one K group of a 32-weight block, from 8 of its 16 packed nibble bytes (each
+// nibble the 4-bit two's complement weight): per byte, ((p ^ 8) + 0x78) ^ 0x80 = sign-extended p,
+// with no carry between bytes. Groups 0 and 1 are the low nibbles of bytes 0-7 and 8-15 (elements
+// 0-15), groups 2 and 3 their high nibbles (elements 16-31).
+__device__ __forceinline__ uint32_t nib8(uint32_t p) {
+    const uint32_t t = (p & 0x0F0F0F0Fu) ^ 0x08080808u;
+    return (t + 0x78787878u) ^ 0x80808080u;
+}
+__device__ __forceinline__ long weights8(uint2 p, int shift) {
+    return (long)(((uint64_t)nib8(p.y >> shift) << 32) | nib8(p.x >> shift));
+}
+
+// Max over each row of 16 lanes (the lanes of one MFMA K group) of non-NaN values.
+__device__ __forceinline__ float row16_max(float m) {
+    m = maxf_bits(m, dpp<0xb1>(__builtin_bit_cast(uint32_t, m)));
+    m = maxf_bits(m, dpp<0x4e>(__builtin_bit_cast(uint32_t, m)));
+    m = maxf_bits(m, dpp<0x141>(__builtin_bit_cast(uint32_t, m)));
+    return maxf_bits(m, dpp<0x140>(__builtin_bit_cast(uint32_t, m)));
+}
+
+// Stages the tile's MTILE activation rows (Q8_0 values, row pitch `pitch` bytes, zeros for the
+// tile's empty places) and their block scales transposed to [block][MTILE].
+__device__ __forceinline__ void stage_rows(const int8_t *__restrict__ src, const float *__restrict__ ssrc, int width,
+                                           const int *row_of, int cnt, int8_t *dst, int pitch, float *sdst) {
+    const int n16 = width / 16, nb = width / QK;
+    for (int i = threadIdx.x; i < MTILE * n16; i += blockDim.x) {
+        const int r = i / n16, c = i - r * n16;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (r < cnt) v = ((const uint4 *)(src + (size_t)row_of[r] * width))[c];
+        *(uint4 *)(dst + r * pitch + c * 16) = v;
+    }
+    for (int i = threadIdx.x; i < MTILE * nb; i += blockDim.x) {
+        const int b = i / MTILE, r = i - b * MTILE;
+        sdst[i] = r < cnt ? ssrc[(size_t)row_of[r] * nb + b] : 0.0f;
     }
 }
 
-template <int PER>
-__global__ __launch_bounds__(G_WAVES * 64) void k_gateup_grouped(
-    const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl, const int32_t *__restrict__ gstart,
-    const int32_t *__restrict__ order, const uint4 *__restrict__ xact, uint32_t *__restrict__ hact, int T,
-    int top_k) {
-    constexpr int S = PER * G_WAVES;
-    using St = StageG<S * 3, G_WAVES * 64>;
-    __shared__ uint4 act[TB][St::SLOTS];
-    __shared__ float terms[64][S + 1];
-    const int t = blockIdx.x, e = blockIdx.y;
-    const int g0 = gstart[e], g1 = gstart[e + 1];
-    if (g0 >= g1) return;
+// The f32 fold of one block into acc: acc[i] = acc[i] + (sumi as f32) * (d_w * d_x[i]).
+__device__ __forceinline__ void fold_block(float (&acc)[4], v4i sumi, float dw, float4 dx) {
+    acc[0] = acc[0] + (float)sumi[0] * (dw * dx.x);
+    acc[1] = acc[1] + (float)sumi[1] * (dw * dx.y);
+    acc[2] = acc[2] + (float)sumi[2] * (dw * dx.z);
+    acc[3] = acc[3] + (float)sumi[3] * (dw * dx.w);
+}
+
+// Gate/up for one 16-pair tile: wave w takes row tile rt = 4 blockIdx.y + w (32 gate rows and the
+// matching 32 up rows, one RVM_PACK_GATE_UP tile). Lane l = 16 g + m holds gate/up rows m and
+// 16 + m for pairs 4g .. 4g + 3 (the MFMA output layout), so each lane folds 16 outputs.
+__global__ __launch_bounds__(MW * 64) void k_gateup_mfma(const uint8_t *__restrict__ nib,
+                                                         const uint16_t *__restrict__ scl,
+                                                         const int32_t *__restrict__ tiles,
+                                                         const int32_t *__restrict__ gstart,
+                                                         const int32_t *__restrict__ order,
+                                                         const int8_t *__restrict__ xq8,
+                                                         const float *__restrict__ xsc, int8_t *__restrict__ hq8,
+                                                         float *__restrict__ hsc, int d, int ff, int top_k) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int row_of[MTILE];
+    const int tile = blockIdx.x;
+    if (tile >= tiles[0]) return;
+    const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
+    const int cnt = min(MTILE, gstart[e + 1] - k0);
+    const int pitch = d + 32, nb = d / QK, Tg = ff / 32;
+    int8_t *Xs = (int8_t *)smem;
+    float *dxs = (float *)(smem + MTILE * pitch);
+    if (threadIdx.x < MTILE) row_of[threadIdx.x] = threadIdx.x < (unsigned)cnt ? order[k0 + threadIdx.x] / top_k : 0;
+    __syncthreads();
+    stage_rows(xq8, xsc, d, row_of, cnt, Xs, pitch, dxs);
+    __syncthreads();
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const size_t base = (((size_t)e * T + t) * S + (size_t)w * PER) * 64 + lane;
-    uint4 wv[PER];
-    uint32_t sv[PER];
+    const int rt = blockIdx.y * MW + w;
+    if (rt >= Tg) return;
+    const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
+    const int shift = (g >> 1) * 4;
+    float acc[4][4] = {};  // gate rows m, 16 + m; up rows m, 16 + m
+    const size_t tbase = ((size_t)e * Tg + rt) * nb * 64;
+    for (int b = 0; b < nb; ++b) {
+        const size_t eb = tbase + (size_t)b * 64;
+        uint2 p[4];
+        uint32_t sc[4];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        wv[i] = nib[base + (size_t)i * 64];
-        sv[i] = scl[base + (size_t)i * 64];
-    }
-    for (int k0 = g0; k0 < g1; k0 += TB) {
-        const int nt = min(TB, g1 - k0);
-        St st[TB];
-#pragma unroll
-        for (int q = 0; q < TB; ++q) {
-            const int tok = order[k0 + (q < nt ? q : 0)] / top_k;
-            st[q].load(xact + (size_t)tok * S * 3, S * 3);
+        for (int r = 0; r < 4; ++r) {
+            const size_t ent = eb + 16 * r + m;  // plane lanes m, 16 + m (gate), 32 + m, 48 + m (up)
+            p[r] = *(const uint2 *)(nib + ent * 16 + (g & 1) * 8);
+            sc[r] = scl[ent];
         }
+        const long a = *(const long *)(Xs + m * pitch + b * QK + g * 8);
+        const float4 dx = *(const float4 *)(dxs + b * MTILE + 4 * g);
 #pragma unroll
-        for (int q = 0; q < TB; ++q) st[q].store(act[q]);
-        __syncthreads();
-        for (int q = 0; q < nt; ++q) {
-            float tv[PER];
-            lane_terms_g<PER>(wv, sv, act[q] + w * PER * 3, tv);
+        for (int r = 0; r < 4; ++r) {
+            const v4i s = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, weights8(p[r], shift), v4i{0, 0, 0, 0}, 0, 0, 0);
+            fold_block(acc[r], s, h2f((uint16_t)sc[r]), dx);
+        }
+    }
+    // GeGLU, then Q8_0 of each pair's 32 h values (rows m and 16 + m over the 16 lanes of group g)
 #pragma unroll
-            for (int i = 0; i < PER; ++i) terms[lane][w * PER + i] = tv[i];
-            __syncthreads();
-            if (w == 0) {
-                float y = 0.0f;  // sequential fold of the row's block terms
-#pragma unroll 8
-                for (int b = 0; b < S; ++b) y = y + terms[lane][b];
-                const float up = __shfl_xor(y, 32);
-                const float h = gelu(y) * up;
-                uint16_t dbits;
-                const int qv = quant_q8_half(h, &dbits);
-                store_prep_half(qv, dbits, lane & 31, hact + ((size_t)(k0 + q) * T + t) * ACT_DW, lane < 32);
-            }
-            __syncthreads();
+    for (int i = 0; i < 4; ++i) {
+        const float h0 = gelu(acc[0][i]) * acc[2][i];
+        const float h1 = gelu(acc[1][i]) * acc[3][i];
+        const float amax = row16_max(fmaxf(fmaxf(0.0f, fabsf(h0)), fabsf(h1)));
+        const float dq = amax / 127.0f;
+        const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
+        const uint16_t dbits = f2h_rne(dq);
+        const int q0 = sat_i8(roundf(h0 * id)), q1 = sat_i8(roundf(h1 * id));
+        const int pr = 4 * g + i;
+        if (pr < cnt) {
+            int8_t *hrow = hq8 + (size_t)(k0 + pr) * ff + rt * 32;
+            hrow[m] = (int8_t)q0;
+            hrow[16 + m] = (int8_t)q1;
+            if (m == 0) hsc[(size_t)(k0 + pr) * Tg + rt] = h2f(dbits);
         }
     }
 }
 
-template <int S>  // steps per lane = ff / 64
-__global__ __launch_bounds__(256) void k_down_grouped(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl,
-                                                      const int32_t *__restrict__ gstart,
-                                                      const uint4 *__restrict__ hact, float *__restrict__ y, int T,
-                                                      int d) {
-    constexpr int NB = 2 * S;
-    using St = StageG<NB * 3, 256>;
-    __shared__ uint4 act[TB][St::SLOTS];
-    const int e = blockIdx.y;
-    const int g0 = gstart[e], g1 = gstart[e + 1];
-    if (g0 >= g1) return;
+// Down for one 16-pair tile: wave w takes the 32-row down tile rt = 4 blockIdx.y + w
+// (RVM_PACK_ROWS32: row r of the tile is plane lane r at block b < S, lane 32 + r at block S + b).
+__global__ __launch_bounds__(MW * 64) void k_down_mfma(const uint8_t *__restrict__ nib,
+                                                       const uint16_t *__restrict__ scl,
+                                                       const int32_t *__restrict__ tiles,
+                                                       const int32_t *__restrict__ gstart,
+                                                       const int8_t *__restrict__ hq8, const float *__restrict__ hsc,
+                                                       float *__restrict__ y, int d, int ff) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int row_of[MTILE];
+    const int tile = blockIdx.x;
+    if (tile >= tiles[0]) return;
+    const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
+    const int cnt = min(MTILE, gstart[e + 1] - k0);
+    const int pitch = ff + 32, nb = ff / QK, Sd = ff / 64, Td = d / 32;
+    int8_t *Hs = (int8_t *)smem;
+    float *dxs = (float *)(smem + MTILE * pitch);
+    if (threadIdx.x < MTILE) row_of[threadIdx.x] = k0 + (threadIdx.x < (unsigned)cnt ? threadIdx.x : 0);
+    __syncthreads();
+    stage_rows(hq8, hsc, ff, row_of, cnt, Hs, pitch, dxs);
+    __syncthreads();
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + w;  // this wave's 32-row tile
-    const int kp = lane >> 5;
-    const size_t base = ((size_t)e * T + t) * S * 64 + lane;
-    uint4 wv[S];
-    uint32_t sv[S];
+    const int rt = blockIdx.y * MW + w;
+    if (rt >= Td) return;
+    const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
+    const int shift = (g >> 1) * 4;
+    float acc[2][4] = {};  // rows m, 16 + m
+    const size_t tbase = ((size_t)e * Td + rt) * Sd * 64;
+    for (int b = 0; b < nb; ++b) {
+        const int half = b >= Sd ? 1 : 0, s = b - half * Sd;
+        const size_t eb = tbase + (size_t)s * 64 + 32 * half;
+        uint2 p[2];
+        uint32_t sc[2];
 #pragma unroll
-    for (int i = 0; i < S; ++i) {
-        wv[i] = nib[base + (size_t)i * 64];
-        sv[i] = scl[base + (size_t)i * 64];
-    }
-    for (int k0 = g0; k0 < g1; k0 += TB) {
-        const int nt = min(TB, g1 - k0);
-        St st[TB];
-#pragma unroll
-        for (int q = 0; q < TB; ++q) st[q].load(hact + (size_t)(k0 + (q < nt ? q : 0)) * NB * 3, NB * 3);
-#pragma unroll
-        for (int q = 0; q < TB; ++q) st[q].store(act[q]);
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < TB; ++q) {
-            float tv[S];
-            lane_terms_g<S>(wv, sv, act[q] + kp * S * 3, tv);
-            float acc = 0.0f;  // block order: this half, then the other half's terms
-#pragma unroll
-            for (int i = 0; i < S; ++i) acc = acc + tv[i];
-#pragma unroll
-            for (int i = 0; i < S; ++i) acc = acc + __shfl_xor(tv[i], 32);
-            if (q < nt && lane < 32) y[(size_t)(k0 + q) * d + (size_t)t * 32 + lane] = acc;
+        for (int r = 0; r < 2; ++r) {
+            const size_t ent = eb + 16 * r + m;
+            p[r] = *(const uint2 *)(nib + ent * 16 + (g & 1) * 8);
+            sc[r] = scl[ent];
         }
-        __syncthreads();
+        const long a = *(const long *)(Hs + m * pitch + b * QK + g * 8);
+        const float4 dx = *(const float4 *)(dxs + b * MTILE + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const v4i s4 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, weights8(p[r], shift), v4i{0, 0, 0, 0}, 0, 0, 0);
+            fold_block(acc[r], s4, h2f((uint16_t)sc[r]), dx);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int pr = 4 * g + i;
+        if (pr < cnt) {
+            float *yrow = y + (size_t)(k0 + pr) * d + rt * 32;
+            yrow[m] = acc[0][i];
+            yrow[16 + m] = acc[1][i];
+        }
     }
 }
 
@@ -182,35 +226,36 @@ extern "C" int rvm_moe_forward(const rvm_layer *L, const float *x, float *out, i
     int32_t *order = (int32_t *)(w + lay.order);
     int32_t *pos_of = (int32_t *)(w + lay.pos_of);
     int32_t *gstart = (int32_t *)(w + lay.gstart);
+    int32_t *tiles = (int32_t *)(w + lay.tiles);
     float *y = (float *)(w + lay.y);
-    const uint4 *xact = (const uint4 *)(w + lay.xact);
-    uint32_t *hact = (uint32_t *)(w + lay.hact);
     int rc = launch_router(L, x, n_tok, flags, eps, w, lay, ids, wts, nullptr, true);
     if (rc) return rc;
     const int pairs = n_tok * L->top_k;
-    if ((rc = launch_plan(ids, pairs, L->n_exp, order, pos_of, gstart))) return rc;
+    if ((rc = launch_plan(ids, pairs, L->n_exp, order, pos_of, gstart, tiles))) return rc;
+    const int nt = (int)max_tiles(L, n_tok);
 
-    const int Tg = 2 * L->ff / 64;
     const size_t gu_entries = (size_t)L->n_exp * 2 * L->ff * (L->d / QK);
-    const uint4 *gnib = (const uint4 *)L->gate_up;
-    const uint16_t *gscl = (const uint16_t *)((const uint8_t *)L->gate_up + gu_entries * 16);
-    rc = with_steps(L->d / 256, [&](auto per) {
-        hipLaunchKernelGGL(k_gateup_grouped<decltype(per)::value>, dim3(Tg, L->n_exp), dim3(G_WAVES * 64), 0,
-                           cur_stream(), gnib, gscl, gstart, order, xact, hact, Tg, L->top_k);
-        return launched();
-    });
-    if (rc) return rc;
+    const uint8_t *gnib = (const uint8_t *)L->gate_up;
+    const uint16_t *gscl = (const uint16_t *)(gnib + gu_entries * 16);
+    const int Tg = L->ff / 32;
+    size_t smem = (size_t)MTILE * (L->d + 32) + (size_t)MTILE * (L->d / QK) * 4;
+    RVM_CHECK(smem <= (size_t)max_lds_per_block());
+    if (smem > 64 * 1024)
+        RVM_TRY(hipFuncSetAttribute((const void *)k_gateup_mfma, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    hipLaunchKernelGGL(k_gateup_mfma, dim3(nt, grid_blocks(Tg, MW)), dim3(MW * 64), smem, cur_stream(), gnib, gscl,
+                       tiles, gstart, order, (const int8_t *)(w + lay.xq8), (const float *)(w + lay.xsc),
+                       (int8_t *)(w + lay.hq8), (float *)(w + lay.hsc), L->d, L->ff, L->top_k);
+    if ((rc = launched())) return rc;
 
-    const int Td = L->d / 32;  // a multiple of 8, so the four-tile groups cover it exactly
     const size_t dn_entries = (size_t)L->n_exp * L->d * (L->ff / QK);
-    const uint4 *dnib = (const uint4 *)L->down;
-    const uint16_t *dscl = (const uint16_t *)((const uint8_t *)L->down + dn_entries * 16);
-    rc = with_steps(L->ff / 64, [&](auto s) {
-        hipLaunchKernelGGL(k_down_grouped<decltype(s)::value>, dim3(Td / 4, L->n_exp), dim3(256), 0, cur_stream(),
-                           dnib, dscl, gstart, (const uint4 *)hact, y, Td, L->d);
-        return launched();
-    });
-    if (rc) return rc;
+    const uint8_t *dnib = (const uint8_t *)L->down;
+    const uint16_t *dscl = (const uint16_t *)(dnib + dn_entries * 16);
+    smem = (size_t)MTILE * (L->ff + 32) + (size_t)MTILE * (L->ff / QK) * 4;
+    RVM_CHECK(smem <= (size_t)max_lds_per_block());
+    hipLaunchKernelGGL(k_down_mfma, dim3(nt, grid_blocks(L->d / 32, MW)), dim3(MW * 64), smem, cur_stream(), dnib,
+                       dscl, tiles, gstart, (const int8_t *)(w + lay.hq8), (const float *)(w + lay.hsc), y, L->d,
+                       L->ff);
+    if ((rc = launched())) return rc;
 
     hipLaunchKernelGGL(k_combine_pairs, dim3(n_tok), dim3(256), 0, cur_stream(), y, pos_of, ids, wts, L->down_scale,
                        out, L->top_k, L->d);

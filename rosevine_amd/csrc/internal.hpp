@@ -32,6 +32,7 @@ constexpr int Q8_BLOCK = 34;
 constexpr int ACT_DW = 12;
 constexpr uint32_t ONES4 = 0x11111111u;
 constexpr int MAX_TOKENS = 65535;  // tokens per call (the router grid's y dimension)
+constexpr int MTILE = 16;          // pairs per tile of the batched (MFMA) expert kernels
 
 // Library state (runtime.hip).
 hipStream_t cur_stream();
@@ -198,10 +199,20 @@ struct WsLayout {
     size_t gstart;  // i32[n_exp + 1]
     size_t y;       // f32[pairs][d] (batched path)
     size_t dterm;   // f32[2 top_k][ff/32][d] (decode: down terms per slot and h block)
+    size_t xq8;     // i8[n_tok][d]: plain Q8_0 values of the layer input (batched path)
+    size_t xsc;     // f32[n_tok][d/32]: their scales
+    size_t hq8;     // i8[pairs][ff]: plain Q8_0 values of h, in plan order (batched path)
+    size_t hsc;     // f32[pairs][ff/32]
+    size_t tiles;   // i32[1 + 2 max_tiles]: the plan's 16-pair tiles
     size_t total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Upper bound on the plan's 16-pair tiles: every group adds at most one partial tile.
+inline size_t max_tiles(const rvm_layer *L, int n_tok) {
+    return ((size_t)n_tok * L->top_k + MTILE - 1) / MTILE + (size_t)L->n_exp;
+}
 
 inline WsLayout ws_layout(const rvm_layer *L, int n_tok) {
     WsLayout w{};
@@ -224,6 +235,11 @@ inline WsLayout ws_layout(const rvm_layer *L, int n_tok) {
     w.y = n_tok > 1 ? take(pairs * L->d * 4) : take(0);
     // kept for every n_tok so that a workspace sized for a batch also serves rvm_moe_decode
     w.dterm = take((size_t)2 * L->top_k * (L->ff / QK) * L->d * 4);
+    w.xq8 = take((size_t)n_tok * L->d);
+    w.xsc = take((size_t)n_tok * (L->d / QK) * 4);
+    w.hq8 = take(pairs * L->ff);
+    w.hsc = take(pairs * (L->ff / QK) * 4);
+    w.tiles = take((1 + 2 * max_tiles(L, n_tok)) * 4);
     w.total = o;
     return w;
 }
@@ -262,6 +278,9 @@ int max_lds_per_block();
 // k_router (logit statistics and the Q8_0 input), then k_select unless select is false.
 int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, float eps, uint8_t *ws,
                   const WsLayout &lay, int32_t *ids, float *wts, float *logits, bool select);
-int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart);
+// k_plan; with tiles set it also lists the 16-pair tiles of every group: tiles[0] = count, then
+// (expert, first position in order) per tile.
+int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart,
+                int32_t *tiles);
 
 }  // namespace rvm

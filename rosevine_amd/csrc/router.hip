@@ -23,7 +23,8 @@ constexpr int SEL_WAVES = 8;  // waves of the selecting workgroup
 template <int F4>
 __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict__ W, const float *__restrict__ x, int n_exp,
                                                 int pre_norm, float eps, double2 *__restrict__ stats,
-                                                uint32_t *__restrict__ xact) {
+                                                uint32_t *__restrict__ xact, int8_t *__restrict__ xq8,
+                                                float *__restrict__ xsc) {
     constexpr int d = 256 * F4, C = 4 * F4, nb = d / QK;
     const int tok = blockIdx.y;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -55,6 +56,10 @@ __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict_
         uint16_t dbits;
         const int q = quant_q8_half(v, &dbits);
         store_prep_half(q, dbits, j, xact + ((size_t)tok * nb + (ok ? hb : 0)) * ACT_DW, ok);
+        if (xq8 && ok) {  // the plain Q8_0 values and scale, for the batched (MFMA) path
+            xq8[((size_t)tok * nb + hb) * QK + j] = (int8_t)q;
+            if (j == 0) xsc[(size_t)tok * nb + hb] = h2f(dbits);
+        }
     }
 
     if (have) {
@@ -117,7 +122,7 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void k_select(const double2 *__rest
 // Ids outside [0, n_exp) are neither counted nor placed (pos_of = -1).
 __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, int n, int n_exp,
                                                int32_t *__restrict__ order, int32_t *__restrict__ pos_of,
-                                               int32_t *__restrict__ gstart) {
+                                               int32_t *__restrict__ gstart, int32_t *__restrict__ tiles) {
     __shared__ int cnt[16][256];
     __shared__ int tot[257];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -137,13 +142,20 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        int run = 0;
+        int run = 0, nt = 0;
         for (int e = 0; e < n_exp; ++e) {
             const int c = tot[e];
             tot[e] = run;
+            if (tiles)  // the group's 16-pair tiles for the batched kernels: (expert, first position)
+                for (int k = 0; k < c; k += MTILE) {
+                    tiles[1 + 2 * nt] = e;
+                    tiles[2 + 2 * nt] = run + k;
+                    ++nt;
+                }
             run += c;
         }
         tot[n_exp] = run;
+        if (tiles) tiles[0] = nt;
     }
     __syncthreads();
     if ((int)threadIdx.x <= n_exp) gstart[threadIdx.x] = tot[threadIdx.x];
@@ -186,7 +198,8 @@ int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, floa
     return with_steps(L->d / 256, [&](auto f4) {
         constexpr int F4 = decltype(f4)::value;
         hipLaunchKernelGGL(k_router<F4>, dim3(groups, n_tok), dim3(RWAVES * 64), 0, cur_stream(), L->router, x, L->n_exp,
-                           pre, eps, (double2 *)(ws + lay.stats), (uint32_t *)(ws + lay.xact));
+                           pre, eps, (double2 *)(ws + lay.stats), (uint32_t *)(ws + lay.xact),
+                           n_tok > 1 ? (int8_t *)(ws + lay.xq8) : nullptr, n_tok > 1 ? (float *)(ws + lay.xsc) : nullptr);
         int rc = launched();
         if (rc || !select) return rc;
         hipLaunchKernelGGL(k_select<F4>, dim3(n_tok), dim3(SEL_WAVES * 64), 0, cur_stream(),
@@ -196,8 +209,10 @@ int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, floa
     });
 }
 
-int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart) {
-    hipLaunchKernelGGL(k_plan, dim3(1), dim3(1024), 0, cur_stream(), ids, n_pairs, n_exp, order, pos_of, gstart);
+int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart,
+                int32_t *tiles) {
+    hipLaunchKernelGGL(k_plan, dim3(1), dim3(1024), 0, cur_stream(), ids, n_pairs, n_exp, order, pos_of, gstart,
+                       tiles);
     return launched();
 }
 
@@ -217,7 +232,7 @@ int rvm_router_select(const rvm_layer *layer, const float *x, int n_tok, int fla
 
 int rvm_moe_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *group_start) {
     RVM_CHECK(ids && order && pos_of && group_start && n_pairs > 0 && n_exp > 0 && n_exp <= 256);
-    return launch_plan(ids, n_pairs, n_exp, order, pos_of, group_start);
+    return launch_plan(ids, n_pairs, n_exp, order, pos_of, group_start, nullptr);
 }
 
 }  // extern "C"
