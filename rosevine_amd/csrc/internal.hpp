@@ -32,7 +32,8 @@ constexpr int Q8_BLOCK = 34;
 constexpr int ACT_DW = 12;
 constexpr uint32_t ONES4 = 0x11111111u;
 constexpr int MAX_TOKENS = 65535;  // tokens per call (the router grid's y dimension)
-constexpr int MTILE = 16;          // pairs per tile of the batched (MFMA) expert kernels
+constexpr int MAX_TOP_K = 8;       // experts per token
+constexpr int MTILE = 16;          // pairs per MFMA m-tile; a batched tile holds 1, 2 or 4 of them
 
 // Library state (runtime.hip).
 hipStream_t cur_stream();
@@ -144,6 +145,20 @@ __device__ __forceinline__ uint32_t swz_xor16(uint32_t v) {
 }
 __device__ __forceinline__ float maxf_bits(float a, uint32_t b) { return fmaxf(a, __builtin_bit_cast(float, b)); }
 
+// Orders LDS traffic between lanes of one wave (a wave's LDS operations complete in issue order).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Byte position of element j of a 32-element Q8_0 block in the batched path's activation rows.
+// MFMA K group g (bytes 8g .. 8g+7) holds elements 4g .. 4g+3 and 16+4g .. 16+4g+3: the elements
+// whose weights sit in the low and high nibbles of byte dword g of a packed Q4_0 entry, so that
+// one dword of the entry is one lane's B operand. The block's int32 sum does not depend on the
+// order of its 32 products.
+__host__ __device__ constexpr int kperm(int j) { return 8 * ((j & 15) >> 2) + 4 * (j >> 4) + (j & 3); }
+
 // Max over each 32-lane half-wave of non-NaN values, returned to every lane of the half.
 __device__ __forceinline__ float half_max(float m) {
     m = maxf_bits(m, dpp<0xb1>(__builtin_bit_cast(uint32_t, m)));
@@ -209,9 +224,9 @@ struct WsLayout {
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Upper bound on the plan's 16-pair tiles: every group adds at most one partial tile.
-inline size_t max_tiles(const rvm_layer *L, int n_tok) {
-    return ((size_t)n_tok * L->top_k + MTILE - 1) / MTILE + (size_t)L->n_exp;
+// Upper bound on the plan's tiles of up to cap pairs: every group adds at most one partial tile.
+inline size_t max_tiles(const rvm_layer *L, int n_tok, int cap) {
+    return ((size_t)n_tok * L->top_k + cap - 1) / cap + (size_t)L->n_exp;
 }
 
 inline WsLayout ws_layout(const rvm_layer *L, int n_tok) {
@@ -239,7 +254,7 @@ inline WsLayout ws_layout(const rvm_layer *L, int n_tok) {
     w.xsc = take((size_t)n_tok * (L->d / QK) * 4);
     w.hq8 = take(pairs * L->ff);
     w.hsc = take(pairs * (L->ff / QK) * 4);
-    w.tiles = take((1 + 2 * max_tiles(L, n_tok)) * 4);
+    w.tiles = take((1 + 2 * max_tiles(L, n_tok, MTILE)) * 4);
     w.total = o;
     return w;
 }
@@ -253,7 +268,7 @@ __host__ __device__ constexpr bool steps_ok(int n) {
 // Layer validation shared by the layer entry points.
 inline bool layer_ok(const rvm_layer *L) {
     return L && L->router && L->gate_up && L->down && L->n_exp > 0 && L->n_exp <= 256 && L->top_k > 0 &&
-           L->top_k <= 8 && L->top_k <= L->n_exp && L->d > 0 && L->d % 256 == 0 && steps_ok(L->d / 256) &&
+           L->top_k <= MAX_TOP_K && L->top_k <= L->n_exp && L->d > 0 && L->d % 256 == 0 && steps_ok(L->d / 256) &&
            L->ff > 0 && L->ff % 64 == 0 && steps_ok(L->ff / 64);
 }
 
@@ -278,9 +293,9 @@ int max_lds_per_block();
 // k_router (logit statistics and the Q8_0 input), then k_select unless select is false.
 int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, float eps, uint8_t *ws,
                   const WsLayout &lay, int32_t *ids, float *wts, float *logits, bool select);
-// k_plan; with tiles set it also lists the 16-pair tiles of every group: tiles[0] = count, then
-// (expert, first position in order) per tile.
+// k_plan; with tiles set it also cuts every group into tiles of up to cap pairs: tiles[0] = count,
+// then (expert, first position in order) per tile, in expert order.
 int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart,
-                int32_t *tiles);
+                int32_t *tiles, int cap);
 
 }  // namespace rvm

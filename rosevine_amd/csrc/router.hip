@@ -56,8 +56,8 @@ __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict_
         uint16_t dbits;
         const int q = quant_q8_half(v, &dbits);
         store_prep_half(q, dbits, j, xact + ((size_t)tok * nb + (ok ? hb : 0)) * ACT_DW, ok);
-        if (xq8 && ok) {  // the plain Q8_0 values and scale, for the batched (MFMA) path
-            xq8[((size_t)tok * nb + hb) * QK + j] = (int8_t)q;
+        if (xq8 && ok) {  // the Q8_0 values in MFMA K order and the scale, for the batched path
+            xq8[((size_t)tok * nb + hb) * QK + kperm(j)] = (int8_t)q;
             if (j == 0) xsc[(size_t)tok * nb + hb] = h2f(dbits);
         }
     }
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void k_select(const double2 *__rest
 // Ids outside [0, n_exp) are neither counted nor placed (pos_of = -1).
 __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, int n, int n_exp,
                                                int32_t *__restrict__ order, int32_t *__restrict__ pos_of,
-                                               int32_t *__restrict__ gstart, int32_t *__restrict__ tiles) {
+                                               int32_t *__restrict__ gstart, int32_t *__restrict__ tiles, int cap) {
     __shared__ int cnt[16][256];
     __shared__ int tot[257];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -141,21 +141,44 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
         tot[threadIdx.x] = s;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0, nt = 0;
-        for (int e = 0; e < n_exp; ++e) {
-            const int c = tot[e];
-            tot[e] = run;
-            if (tiles)  // the group's 16-pair tiles for the batched kernels: (expert, first position)
-                for (int k = 0; k < c; k += MTILE) {
-                    tiles[1 + 2 * nt] = e;
-                    tiles[2 + 2 * nt] = run + k;
-                    ++nt;
-                }
-            run += c;
+    if (w == 0) {  // exclusive scans of the group sizes and of their tile counts, 4 experts a lane
+        int c[4], t[4], cs = 0, ts = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int e = 4 * lane + k;
+            c[k] = e < n_exp ? tot[e] : 0;
+            t[k] = (c[k] + cap - 1) / cap;
+            cs += c[k];
+            ts += t[k];
         }
-        tot[n_exp] = run;
-        if (tiles) tiles[0] = nt;
+        int ic = cs, it = ts;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int nc = __shfl_up(ic, o), nt = __shfl_up(it, o);
+            if (lane >= o) {
+                ic += nc;
+                it += nt;
+            }
+        }
+        int run = ic - cs, nt = it - ts;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int e = 4 * lane + k;
+            if (e < n_exp) {
+                tot[e] = run;
+                if (tiles)  // the group's tiles for the batched kernels: (expert, first position)
+                    for (int q = 0; q < t[k]; ++q) {
+                        tiles[1 + 2 * (nt + q)] = e;
+                        tiles[2 + 2 * (nt + q)] = run + q * cap;
+                    }
+            }
+            run += c[k];
+            nt += t[k];
+        }
+        if (lane == 63) {
+            tot[n_exp] = ic;
+            if (tiles) tiles[0] = it;
+        }
     }
     __syncthreads();
     if ((int)threadIdx.x <= n_exp) gstart[threadIdx.x] = tot[threadIdx.x];
@@ -210,9 +233,10 @@ int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, floa
 }
 
 int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart,
-                int32_t *tiles) {
+                int32_t *tiles, int cap) {
+    RVM_CHECK(cap >= 1);
     hipLaunchKernelGGL(k_plan, dim3(1), dim3(1024), 0, cur_stream(), ids, n_pairs, n_exp, order, pos_of, gstart,
-                       tiles);
+                       tiles, cap);
     return launched();
 }
 
@@ -232,7 +256,7 @@ int rvm_router_select(const rvm_layer *layer, const float *x, int n_tok, int fla
 
 int rvm_moe_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *group_start) {
     RVM_CHECK(ids && order && pos_of && group_start && n_pairs > 0 && n_exp > 0 && n_exp <= 256);
-    return launch_plan(ids, n_pairs, n_exp, order, pos_of, group_start, nullptr);
+    return launch_plan(ids, n_pairs, n_exp, order, pos_of, group_start, nullptr, MTILE);
 }
 
 }  // extern "C"

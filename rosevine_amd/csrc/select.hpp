@@ -55,12 +55,6 @@ __device__ __forceinline__ float wave_max_f(float v) {
     return v;
 }
 
-// Orders LDS traffic between lanes of one wave (a wave's LDS operations complete in issue order).
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Rust f32::total_cmp key, and an unsigned key with the same order (for packed ranking).
 __device__ __forceinline__ int32_t total_key(float f) {
