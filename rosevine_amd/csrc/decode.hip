@@ -85,6 +85,11 @@ __device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const
     constexpr int S = PER * GU_WAVES, d = 256 * PER, RD = (d + GU_WAVES * 64 - 1) / (GU_WAVES * 64);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
+    // The activation blocks go to LDS before the weight loads are issued: a barrier behind a
+    // wave's full set of weight loads would wait until the memory pipeline had taken them all,
+    // and the block terms below are formed as their weights arrive.
+    if (STAGE) st.store(act);
+    __syncthreads();  // act is staged; and the previous user of terms and hprep is done
     const size_t base = (((size_t)e * T + t) * S + (size_t)w * PER) * 64 + lane;
     uint4 wv[PER];
     uint32_t sv[PER];
@@ -106,8 +111,6 @@ __device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const
         ds[i] = dscl[ent];
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (STAGE) st.store(act);
-    __syncthreads();  // act is staged; and the previous user of terms and hprep is done
     float tv[PER];
     lane_terms<PER>(wv, sv, act + w * PER * 3, tv);
 #pragma unroll

@@ -180,6 +180,9 @@ struct SelShared {
     int pass;
     alignas(16) float xs[256 * F4];  // the exact path's layer input (x, or rms_norm(x))
     alignas(16) float P[128 * 36];   // the exact path's products: 128 rows x 32 columns, pitch 36
+    int cand[32];                    // the candidate path's experts, ascending
+    float csp[32], csel[9];          // their softmax numerators; ranks 0 .. 8 in order
+    int ncand, cok;
 };
 
 // Exact reference-order logits of every expert into sh.sR: the f32 products W_r[e][i] * x'[i]
@@ -247,6 +250,190 @@ __device__ void exact_all(SelShared<F4, NW> &sh, const float *__restrict__ W, co
         if (w < 2 && fe < n_exp) sh.sR[fe] = bias ? acc + bias[fe] : acc;
     }
     __syncthreads();
+}
+
+// Exact ids from the experts that can still reach the top k, when the certificate fails
+// (runtime/src/exec.rs:507-517, ops.rs:170-187). L = the lowest lower bound S - E among the top
+// k of the S ranking; every expert whose upper bound is within order_margin of L is a candidate
+// (at most 16; ties among the top keys or non-finite statistics leave this to exact_all). Lane c
+// of wave 0 folds candidate c's logit in the reference's order, so the candidates' softmax
+// numerators expf(R - max) are the reference's. The reference ranks p = numerator * (1/sum as
+// f32); sum depends on every expert and is not known exactly here, but the ranking does not
+// depend on it when the numerators at ranks 0 .. top_k are equal or clearly apart, and every
+// other expert's largest numerator is clearly below the k-th; that is checked. The weights are
+// then formed as on the certified path (tolerance class). Returns false (nothing selected) when
+// a check fails; then sh.sel and sh.wsel are the exact_all path's to fill. Called by every thread.
+template <int F4, int NW>
+__device__ bool exact_candidates(SelShared<F4, NW> &sh, const float *__restrict__ W, const float *__restrict__ bias,
+                                 const float *__restrict__ xt, int n_exp, int top_k, int pre_norm, float eps) {
+    constexpr int d = 256 * F4, CM = 16, CK = 128, NCH = d / CK, PP = CK + 4, D = 6;
+    static_assert(2 * CM * PP <= 128 * 36, "two product buffers fit the exact path's LDS");
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    uint64_t cmask[4] = {0, 0, 0, 0};  // wave 0: the candidates among experts l + 64 i
+    if (w == 0) {
+        bool ok = true;
+        for (int j = 0; j < top_k; ++j) ok = ok && sh.hits[j] == 1;
+        for (int i = 0; i < NW; ++i) ok = ok && sh.badw[i] == 0;
+        double L = INFINITY;
+        for (int j = 0; j < top_k; ++j) L = fmin(L, sh.selS[j] - sh.selE[j]);
+        const double M = sh.selS[0];
+        int nc = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = lane + 64 * i;
+            bool c = false;
+            if (e < n_exp) {
+                const double S = sh.Sx[e], E = sh.Ex[e];
+                c = S + E + order_margin(S, L, M) >= L;
+            }
+            cmask[i] = __ballot(c);
+            const int pos = nc + __popcll(cmask[i] & ((1ull << lane) - 1ull));
+            if (c && pos < CM) sh.cand[pos] = e;
+            nc += __popcll(cmask[i]);
+        }
+        if (lane == 0) sh.ncand = ok && nc <= CM ? nc : -1;
+    } else if (w == 1) {
+        float4 xv[F4];
+        load_x_chunk<F4>(xt, lane, pre_norm, eps, xv);
+#pragma unroll
+        for (int i = 0; i < F4; ++i) ((float4 *)sh.xs)[lane * F4 + i] = xv[i];
+    }
+    __syncthreads();
+    const int nc = sh.ncand;
+    if (nc < 0) return false;
+    // The candidates' logits: f32 products added in element order from -0.0, then the bias. Waves
+    // 1.. form the products of CK-column chunks into LDS (double-buffered; each thread keeps its
+    // loads D chunks ahead in a register ring), and lane c of wave 0 adds candidate c's.
+    constexpr int NPT = 64 * (NW - 1), IT = (CM * CK / 4 + NPT - 1) / NPT;
+    const int pt = tid - 64;
+    const float *src[IT];
+    int dst[IT], col[IT];
+    bool vok[IT];
+#pragma unroll
+    for (int k = 0; k < IT; ++k) {
+        const int i = pt + k * NPT;
+        vok[k] = pt >= 0 && i < nc * (CK / 4);
+        const int ii = vok[k] ? i : 0, c = ii / (CK / 4), q = ii - c * (CK / 4);
+        src[k] = W + (size_t)sh.cand[c] * d + 4 * q;
+        dst[k] = c * PP + 4 * q;
+        col[k] = 4 * q;
+    }
+    auto load = [&](int ch, float4 (&r)[IT]) {  // unconditional: the chunk index is clamped
+        const int cc = min(ch, NCH - 1);
+#pragma unroll
+        for (int k = 0; k < IT; ++k) r[k] = *(const float4 *)(src[k] + cc * CK);
+    };
+    auto store = [&](int ch, int buf, const float4 (&r)[IT]) {
+#pragma unroll
+        for (int k = 0; k < IT; ++k)
+            if (vok[k]) {
+                const float4 xv = *(const float4 *)(sh.xs + ch * CK + col[k]);
+                *(float4 *)(sh.P + buf * CM * PP + dst[k]) =
+                    make_float4(r[k].x * xv.x, r[k].y * xv.y, r[k].z * xv.z, r[k].w * xv.w);
+            }
+    };
+    float acc = -0.0f;
+    auto fold = [&](int buf) {
+        if (w != 0) return;
+        const float4 *pr = (const float4 *)(sh.P + buf * CM * PP + min(lane, nc - 1) * PP);
+#pragma unroll
+        for (int g = 0; g < CK / 32; ++g) {
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = pr[g * 8 + j];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                acc = acc + v[j].x;
+                acc = acc + v[j].y;
+                acc = acc + v[j].z;
+                acc = acc + v[j].w;
+            }
+        }
+    };
+    float4 ring[D][IT];
+#pragma unroll
+    for (int u = 0; u < D; ++u) load(u, ring[u]);
+    store(0, 0, ring[0]);
+    __syncthreads();
+    for (int c0 = 0; c0 < NCH; c0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int c = c0 + u;
+            if (c < NCH) {
+                load(c + D, ring[u]);  // ring[u] held chunk c, stored one step ago
+                fold(c & 1);
+                if (c + 1 < NCH) store(c + 1, (c + 1) & 1, ring[(u + 1) % D]);
+                __syncthreads();
+            }
+        }
+    }
+    if (w == 0) {
+        const int ce = sh.cand[min(lane, nc - 1)];
+        const float R = bias ? acc + bias[ce] : acc;
+        const float Mf = wave_max_f(lane < nc ? R : -INFINITY);  // the largest logit is a candidate's
+        const float spc = (float)exp((double)(R - Mf));         // exactly the reference's numerator
+        // rank of each candidate by (numerator desc, index asc); the candidates are in index order
+        if (lane < nc) sh.csp[lane] = spc;
+        wave_lds_sync();
+        int rk = 64;
+        if (lane < nc) {
+            const uint32_t k = order_key(spc);
+            rk = 0;
+            for (int c2 = 0; c2 < nc; ++c2) {
+                const uint32_t k2 = order_key(sh.csp[c2]);
+                rk += (k2 > k || (k2 == k && c2 < lane)) ? 1 : 0;
+            }
+            if (rk <= top_k) sh.csel[rk] = spc;
+        }
+        wave_lds_sync();
+        // The reference orders p = numerator * inv. Multiplying by one positive inv keeps equal
+        // numerators equal (their order is by index, as here) and keeps numerators more than a
+        // factor 1 + 2^-21 apart strictly ordered, whatever inv is; closer pairs at ranks
+        // 0 .. top_k, or an expert outside the candidates closer than that to the k-th, are left
+        // to exact_all.
+        const float sep = 1.0f + 0x1p-21f;
+        bool ok = true;
+        if (lane < nc && rk < top_k) {
+            const float next = rk + 1 < nc ? sh.csel[rk + 1] : 0.0f;
+            ok = spc == next || spc > next * sep;
+        }
+        const float pk = sh.csel[top_k - 1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = lane + 64 * i;
+            if (e < n_exp && !((cmask[i] >> lane) & 1ull)) {
+                const float hi = round_up_f32(sh.Sx[e] + sh.Ex[e]);
+                ok = ok && (float)exp((double)(hi - Mf)) * sep < pk;
+            }
+        }
+        ok = __ballot(!ok) == 0;
+        if (lane < nc && rk < top_k) sh.sel[rk] = ce;
+        // weights (tolerance class, as on the certified path): the candidates' exact numerators,
+        // the others' from the estimates, an f64 sum in index order, renormalised over the top k
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = lane + 64 * i;
+            if (e < n_exp) sh.sp[e] = (float)exp((double)((float)sh.Sx[e] - Mf));
+        }
+        wave_lds_sync();
+        if (lane < nc) sh.sp[ce] = spc;
+        wave_lds_sync();
+        double sum = 0.0;
+        if (lane == 0)
+            for (int j = 0; j < n_exp; ++j) sum += (double)sh.sp[j];
+        const float inv = (float)(1.0 / __shfl(sum, 0));
+        if (ok && lane < top_k) {
+            float s = -0.0f;
+            for (int j = 0; j < top_k; ++j) s = s + sh.csel[j] * inv;
+            s = fmaxf(s, 1.0f / 16384.0f);
+            sh.wsel[lane] = sh.csel[lane] * inv / s;
+        }
+        if (lane == 0) sh.cok = ok;
+    }
+    __syncthreads();
+    return sh.cok != 0;
 }
 
 // Selects top_k experts for one token. st: the token's [n_exp] statistics; xt: its layer input.
@@ -389,11 +576,14 @@ __device__ void select_token(SelShared<F4, NW> &sh, const double2 *__restrict__ 
     }
     __syncthreads();
     if (!sh.pass && exact_here) {
-        // ---- exact path: every logit in the reference's order, then the reference's softmax
+        // ---- exact path: the candidates first (exact_candidates); else every logit in the
+        // reference's order, then the reference's softmax
         // (runtime/src/ops.rs:170-179: f64 sum in index order, expf correctly rounded) and top_k
         // by total_cmp (ops.rs:182-187) ----
-        exact_all<F4, NW>(sh, W, bias, xt, n_exp, pre_norm, eps);
-        if (w == 0) {
+        const bool done = !(publish && lg_t) &&
+                          exact_candidates<F4, NW>(sh, W, bias, xt, n_exp, top_k, pre_norm, eps);
+        if (!done) exact_all<F4, NW>(sh, W, bias, xt, n_exp, pre_norm, eps);
+        if (!done && w == 0) {
             float R[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) R[i] = lane + 64 * i < n_exp ? sh.sR[lane + 64 * i] : -INFINITY;

@@ -100,6 +100,27 @@ def test_router_certified_ids_match_oracle(gpu, orc):
         assert ws2.fallbacks() == n
 
 
+def test_router_exact_candidates_match_the_full_exact_path(gpu, orc):
+    """EXACT_SELECT without logits takes the candidate path (exact folds of the experts that can
+    reach the top k, ranking certified for any softmax denominator); with logits every expert is
+    folded. Both give the reference's ids; the candidate path's weights are tolerance class."""
+    for bias in (False, True):
+        key = get_layer(0, bias=bias)
+        L, router, b = key[0], key[1], key[2]
+        n = 1024
+        x = synth.tokens(SEED + 2, n)
+        want_ids, want_w, _ = orc.select_experts(orc.router_logits(router, b, x, N_EXP, D), TOP_K)
+        ws = moe.Workspace(L, n)
+        ids, w = moe.router_select(L, dev(x), n, ws, flags=hip.EXACT_SELECT)
+        ws2 = moe.Workspace(L, n)
+        ids2, w2, _ = moe.router_select(L, dev(x), n, ws2, flags=hip.EXACT_SELECT, with_logits=True)
+        assert np.array_equal(ids, want_ids.astype(np.int32))
+        assert np.array_equal(ids2, ids)
+        assert np.max(np.abs(w - w2)) <= 1e-6
+        assert np.max(np.abs(w - want_w)) <= 1e-6
+        assert ws.fallbacks() == n
+
+
 def test_router_ties_go_to_the_lower_index(gpu, orc):
     rng = np.random.default_rng(5)
     router = (rng.standard_normal((N_EXP, D)) * 0.02).astype(np.float32)
