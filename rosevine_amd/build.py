@@ -28,6 +28,9 @@ FLAGS = [
     "-Werror",
     "-Wno-unused-command-line-argument",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the batched kernels convert every block sum right away, and the
+    # accumulation-register form costs a read per value
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -24,9 +24,10 @@ namespace rvm {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int MW = 4;             // waves (row tiles) per workgroup
-constexpr int KC = 4;             // K blocks per chunk
-constexpr int XP = KC * QK + 16;  // LDS pitch of a staged activation row: conflict-free 8-byte reads
+constexpr int MW = 4;  // waves (row tiles) per workgroup
+// K blocks per chunk (a template parameter of the tile loop; 8 measured slower for one m-tile)
+template <int MT>
+constexpr int chunk_blocks() { return 4; }
 
 // 8 int8 weights from one dword of a packed Q4_0 entry (bytes 4g .. 4g+3, each nibble the 4-bit
 // two's complement weight): the low nibbles (elements 4g .. 4g+3) then the high nibbles
@@ -56,9 +57,9 @@ __device__ __forceinline__ void fold_block(float (&acc)[4], v4i sumi, float dw, 
     acc[3] = acc[3] + (float)sumi[3] * (dw * dx.w);
 }
 
-template <int MT, int NR>
+template <int MT, int NR, int KC>
 struct TileLds {
-    static constexpr int R = 16 * MT;
+    static constexpr int R = 16 * MT, XP = KC * QK + 16;  // row pitch: conflict-free 8-byte reads
     alignas(16) int8_t xs[2][R * XP];           // activation rows of the chunk
     alignas(16) float ss[2][KC * R];            // their block scales, [block][row]
     alignas(16) uint16_t ws[MW][KC * 16 * NR];  // per wave: weight scales, [block][m][piece]
@@ -70,18 +71,18 @@ struct TileLds {
 // activation rows (K = width, nb = width / 32 blocks). acc[mt][r][i] is the output of pair
 // 16 mt + 4 g + i and plane lane 16 r + m, for lane = 16 g + m. All waves take part in the staging
 // and barriers; waves without a row tile (active false) skip the weights and MFMAs.
-template <int MT, int NR>
+template <int MT, int NR, int KC>
 __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const uint16_t *__restrict__ scl,
                                           size_t tb, int S, bool active, const int8_t *__restrict__ src,
-                                          const float *__restrict__ ssrc, int width, TileLds<MT, NR> &sh,
+                                          const float *__restrict__ ssrc, int width, TileLds<MT, NR, KC> &sh,
                                           float (&acc)[MT][NR][4]) {
     // Every global load below is issued unconditionally (addresses clamped into the buffers, the
     // values selected when stored), so that the compiler can count the loads in flight and wait
     // for exactly the ones it needs: the next chunk's loads stay outstanding while this one runs.
-    constexpr int R = 16 * MT, NT = MW * 64;
+    constexpr int R = 16 * MT, NT = MW * 64, XP = TileLds<MT, NR, KC>::XP;
     constexpr int XU = KC * QK / 16;  // 16-byte pieces of a staged row chunk
     constexpr int XI = (R * XU + NT - 1) / NT, SI = (R * KC + NT - 1) / NT;
-    constexpr int SPL = KC * 16 * NR / 64;  // weight scales per lane per chunk (4 or 2)
+    constexpr int SPL = KC * 16 * NR / 64;  // weight scales per lane per chunk (2, 4 or 8)
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
     const int w = threadIdx.x >> 6;
     const int nb = width / QK, nch = (nb + KC - 1) / KC;
@@ -97,8 +98,10 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
         const int half = b >= S ? 1 : 0;
         return (tb + (size_t)(b - half * S)) * 64 + 32 * half;
     };
-    // this lane's share of a chunk's weight scales: block kb = lane / 16, entries j .. j+SPL-1
-    const int skb = lane >> 4, sj = (lane & 15) * SPL;
+    // this lane's share of a chunk's weight scales: block kb = lane / (64 / KC), entries
+    // j .. j+SPL-1 of it
+    constexpr int LPB = 64 / KC;
+    const int skb = lane / LPB, sj = (lane % LPB) * SPL;
     // this thread's staging items, fixed over the chunks: activation piece q of tile place xrow[k],
     // and the scale of place srow[k] at chunk block skbx[k]
     const int8_t *xsrc[XI];
@@ -133,7 +136,13 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
             for (int r = 0; r < NR; ++r) wn[kb][r] = *(const uint32_t *)(nib + (e0 + 16 * r + m) * 16 + 4 * g);
         }
         const uint16_t *sp = scl + entry(c * KC + skb) + sj;
-        if constexpr (SPL == 4) {
+        if constexpr (SPL == 8) {
+            const uint4 v = *(const uint4 *)sp;
+            wsc[0] = v.x;
+            wsc[1] = v.y;
+            wsc[2] = v.z;
+            wsc[3] = v.w;
+        } else if constexpr (SPL == 4) {
             const uint2 v = *(const uint2 *)sp;
             wsc[0] = v.x;
             wsc[1] = v.y;
@@ -193,15 +202,19 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
                 a[mt] = *(const long *)(sh.xs[buf] + (mt * 16 + m) * XP + kb * QK + g * 8);
                 dx[mt] = *(const float4 *)(sh.ss[buf] + kb * R + mt * 16 + 4 * g);
             }
+            // every MFMA of the block first, then the folds: no fold waits on the MFMA just issued
+            v4i sm[MT][NR];
 #pragma unroll
             for (int r = 0; r < NR; ++r) {
                 const long bw = weights8(wn[kb][r]);
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const v4i s = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[mt], bw, v4i{0, 0, 0, 0}, 0, 0, 0);
-                    fold_block(acc[mt][r], s, dw[r], dx[mt]);
-                }
+                for (int mt = 0; mt < MT; ++mt)
+                    sm[mt][r] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[mt], bw, v4i{0, 0, 0, 0}, 0, 0, 0);
             }
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) fold_block(acc[mt][r], sm[mt][r], dw[r], dx[mt]);
         }
         wave_lds_sync();  // the next chunk's scale stores stay behind these reads
     };
@@ -250,8 +263,8 @@ __global__ __launch_bounds__(MW * 64) void k_gateup_mfma(const uint8_t *__restri
                                                          const int8_t *__restrict__ xq8,
                                                          const float *__restrict__ xsc, int8_t *__restrict__ hq8,
                                                          float *__restrict__ hsc, int d, int ff, int top_k) {
-    constexpr int R = 16 * MT;
-    __shared__ TileLds<MT, 4> sh;
+    constexpr int R = 16 * MT, KC = chunk_blocks<MT>();
+    __shared__ TileLds<MT, 4, KC> sh;
     const int tile = blockIdx.x;
     if (tile >= tiles[0]) return;
     const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
@@ -262,11 +275,12 @@ __global__ __launch_bounds__(MW * 64) void k_gateup_mfma(const uint8_t *__restri
     const int rt = blockIdx.y * MW + (threadIdx.x >> 6);
     const bool active = rt < Tg;
     float acc[MT][4][4];
-    tile_sums<MT, 4>(nib, scl, ((size_t)e * Tg + (active ? rt : 0)) * nb, nb, active, xq8, xsc, d, sh, acc);
+    tile_sums<MT, 4, KC>(nib, scl, ((size_t)e * Tg + (active ? rt : 0)) * nb, nb, active, xq8, xsc, d, sh, acc);
     if (!active) return;
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt) {
+        if (mt * 16 >= cnt) break;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float h0 = gelu(acc[mt][0][i]) * acc[mt][2][i];
@@ -284,6 +298,7 @@ __global__ __launch_bounds__(MW * 64) void k_gateup_mfma(const uint8_t *__restri
                 if (m == 0) hsc[(size_t)(k0 + pr) * Tg + rt] = h2f(dbits);
             }
         }
+    }
 }
 
 // Down for one tile: wave w takes the 32-row down tile rt = 4 blockIdx.y + w (RVM_PACK_ROWS32:
@@ -296,8 +311,8 @@ __global__ __launch_bounds__(MW * 64) void k_down_mfma(const uint8_t *__restrict
                                                        const int32_t *__restrict__ gstart,
                                                        const int8_t *__restrict__ hq8, const float *__restrict__ hsc,
                                                        float *__restrict__ y, int d, int ff) {
-    constexpr int R = 16 * MT;
-    __shared__ TileLds<MT, 2> sh;
+    constexpr int R = 16 * MT, KC = chunk_blocks<MT>();
+    __shared__ TileLds<MT, 2, KC> sh;
     const int tile = blockIdx.x;
     if (tile >= tiles[0]) return;
     const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
@@ -308,7 +323,7 @@ __global__ __launch_bounds__(MW * 64) void k_down_mfma(const uint8_t *__restrict
     const int rt = blockIdx.y * MW + (threadIdx.x >> 6);
     const bool active = rt < Td;
     float acc[MT][2][4];
-    tile_sums<MT, 2>(nib, scl, ((size_t)e * Td + (active ? rt : 0)) * Sd, Sd, active, hq8, hsc, ff, sh, acc);
+    tile_sums<MT, 2, KC>(nib, scl, ((size_t)e * Td + (active ? rt : 0)) * Sd, Sd, active, hq8, hsc, ff, sh, acc);
     if (!active) return;
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -369,7 +384,6 @@ __global__ __launch_bounds__(256) void k_combine_pairs(const float *__restrict__
 // streamed once.
 inline int tile_mt(const rvm_layer *L, int n_tok) {
     const long pairs = (long)n_tok * L->top_k;
-    if (pairs >= 24L * L->n_exp) return 4;
     if (pairs >= 8L * L->n_exp) return 2;
     return 1;
 }

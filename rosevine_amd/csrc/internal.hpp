@@ -207,8 +207,8 @@ struct WsLayout {
     size_t stats;   // double2[n_tok][n_exp]: exact-sum estimate and error bound per logit
     size_t ids;     // i32[n_tok][top_k]
     size_t wts;     // f32[n_tok][top_k]
-    size_t xact;    // u32[n_tok][d/32][ACT_DW]
-    size_t hact;    // u32[pairs + top_k][ff/32][ACT_DW]
+    size_t xact;    // u32[d/32][ACT_DW]: the decode token's prepared activation blocks
+    size_t hact;    // u32[2 top_k][ff/32][ACT_DW]: decode h blocks per slot, then correction rows
     size_t order;   // i32[pairs]
     size_t pos_of;  // i32[pairs]
     size_t gstart;  // i32[n_exp + 1]
@@ -242,8 +242,8 @@ inline WsLayout ws_layout(const rvm_layer *L, int n_tok) {
     w.stats = take((size_t)n_tok * L->n_exp * 16);
     w.ids = take(pairs * 4);
     w.wts = take(pairs * 4);
-    w.xact = take((size_t)n_tok * (L->d / QK) * ACT_DW * 4);
-    w.hact = take((pairs + L->top_k) * (L->ff / QK) * ACT_DW * 4);  // + decode correction rows
+    w.xact = take((size_t)(L->d / QK) * ACT_DW * 4);
+    w.hact = take((size_t)2 * L->top_k * (L->ff / QK) * ACT_DW * 4);  // slots + correction rows
     w.order = take(pairs * 4);
     w.pos_of = take(pairs * 4);
     w.gstart = take((size_t)(L->n_exp + 1) * 4);

@@ -19,13 +19,76 @@ namespace rvm {
 constexpr int RWAVES = 1;  // waves (experts) per router workgroup: one expert per CU spreads the row loads
 constexpr int SEL_WAVES = 8;  // waves of the selecting workgroup
 
-// F4 = d / 256: lane l owns elements [4*F4*l, 4*F4*(l+1)) of a router row.
+// The logit statistics of one router row and one token: S = the f64 sum of the f32 products
+// (lane chunks summed in order, then a wave scan), and the bound on the sequential f32 fold's
+// error from the prefix sums. Every lane returns the same pair.
+template <int F4>
+__device__ __forceinline__ double2 row_stats(const float4 (&wv)[F4], const float4 (&xv)[F4], int lane) {
+    constexpr int d = 256 * F4, C = 4 * F4;
+    float p[C];
+#pragma unroll
+    for (int i = 0; i < F4; ++i) {
+        p[4 * i] = wv[i].x * xv[i].x;
+        p[4 * i + 1] = wv[i].y * xv[i].y;
+        p[4 * i + 2] = wv[i].z * xv[i].z;
+        p[4 * i + 3] = wv[i].w * xv[i].w;
+    }
+    double c = 0.0;
+#pragma unroll
+    for (int i = 0; i < C; ++i) c += (double)p[i];
+    double incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double n = __shfl_up(incl, o);
+        if (lane >= o) incl += n;
+    }
+    double run = __shfl_up(incl, 1);
+    if (lane == 0) run = 0.0;
+    const double total = __shfl(incl, 63);
+    double babs = 0.0;
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        run += (double)p[i];
+        babs += fabs(run);
+    }
+    babs = wave_sum_d(babs);
+    const double u = 0x1p-24, g = u / (1.0 - u);
+    return make_double2(total, babs * g / (1.0 - (double)d * g) * (1.0 + 0x1p-20) + 1e-300);
+}
+
+// Q8_0 quantisation of the layer input xt (its rms_norm scale already known), one 32-block per
+// half-wave (runtime/src/ops.rs:95-105): blocks base0 + lane / 32, base0 + step + lane / 32, ...
+// to the prepared decode blocks (xact) and, when xq8 is set, the plain values in MFMA K order
+// and their scales.
+template <int F4>
+__device__ __forceinline__ void quant_x_blocks(const float *__restrict__ xt, int pre_norm, float scale, int base0,
+                                               int step, float first, uint32_t *__restrict__ xact,
+                                               int8_t *__restrict__ xq8, float *__restrict__ xsc, int lane) {
+    constexpr int nb = 256 * F4 / QK;
+    const int j = lane & 31;
+    for (int base = base0; base < nb; base += step) {
+        const int hb = base + (lane >> 5);
+        const bool ok = hb < nb;
+        float v = base == base0 ? first : (ok ? xt[hb * QK + j] : 0.0f);
+        if (pre_norm) v = v * scale;
+        uint16_t dbits;
+        const int q = quant_q8_half(v, &dbits);
+        if (xact) store_prep_half(q, dbits, j, xact + (size_t)(ok ? hb : 0) * ACT_DW, ok);
+        if (xq8 && ok) {
+            xq8[hb * QK + kperm(j)] = (int8_t)q;
+            if (j == 0) xsc[hb] = h2f(dbits);
+        }
+    }
+}
+
+// One token (blockIdx.y), one expert per wave. F4 = d / 256: lane l owns elements
+// [4 F4 l, 4 F4 (l + 1)) of a router row.
 template <int F4>
 __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict__ W, const float *__restrict__ x, int n_exp,
                                                 int pre_norm, float eps, double2 *__restrict__ stats,
                                                 uint32_t *__restrict__ xact, int8_t *__restrict__ xq8,
                                                 float *__restrict__ xsc) {
-    constexpr int d = 256 * F4, C = 4 * F4, nb = d / QK;
+    constexpr int d = 256 * F4, nb = d / QK;
     const int tok = blockIdx.y;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -38,62 +101,64 @@ __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict_
     const float4 *w4 = (const float4 *)(W + (size_t)(have ? e : 0) * d) + lane * F4;
 #pragma unroll
     for (int i = 0; i < F4; ++i) wv[i] = w4[i];
-    const int hw_total = gridDim.x * RWAVES * 2;
     const int base0 = (blockIdx.x * RWAVES + w) * 2;
-    const int j = lane & 31;
     const int hb0 = base0 + (lane >> 5);
-    const float qv0 = hb0 < nb ? xt[hb0 * QK + j] : 0.0f;
+    const float qv0 = hb0 < nb ? xt[hb0 * QK + (lane & 31)] : 0.0f;
     float4 xv[F4];
     const float scale = load_x_chunk<F4>(xt, lane, pre_norm, eps, xv);
-
-    // Q8_0 quantisation of the layer input, one 32-block per half-wave (runtime/src/ops.rs:95-105),
-    // while the row loads are in flight.
-    for (int base = base0; base < nb; base += hw_total) {
-        const int hb = base + (lane >> 5);
-        const bool ok = hb < nb;
-        float v = base == base0 ? qv0 : (ok ? xt[hb * QK + j] : 0.0f);
-        if (pre_norm) v = v * scale;
-        uint16_t dbits;
-        const int q = quant_q8_half(v, &dbits);
-        store_prep_half(q, dbits, j, xact + ((size_t)tok * nb + (ok ? hb : 0)) * ACT_DW, ok);
-        if (xq8 && ok) {  // the Q8_0 values in MFMA K order and the scale, for the batched path
-            xq8[((size_t)tok * nb + hb) * QK + kperm(j)] = (int8_t)q;
-            if (j == 0) xsc[(size_t)tok * nb + hb] = h2f(dbits);
-        }
-    }
-
+    // the quantisation runs while the row loads are in flight
+    quant_x_blocks<F4>(xt, pre_norm, scale, base0, gridDim.x * RWAVES * 2, qv0, xact + (size_t)tok * nb * ACT_DW,
+                       xq8 ? xq8 + (size_t)tok * d : nullptr, xq8 ? xsc + (size_t)tok * nb : nullptr, lane);
     if (have) {
-        float p[C];
+        const double2 st = row_stats<F4>(wv, xv, lane);
+        if (lane == 0) stats[(size_t)tok * n_exp + e] = st;
+    }
+}
+
+// Batched statistics: workgroup (g, r) keeps the rows of experts BW g .. BW g + BW-1 in registers
+// (one per wave) and takes tokens r RT .. r RT + RT-1, the next token's x loads in flight while
+// the current one is processed; the numbers are row_stats', as in k_router. The Q8_0 blocks of
+// each token are shared out over the expert groups.
+constexpr int BW = 4;
+template <int F4>
+__global__ __launch_bounds__(BW * 64) void k_router_batch(const float *__restrict__ W, const float *__restrict__ x,
+                                                          int n_tok, int n_exp, int RT, int pre_norm, float eps,
+                                                          double2 *__restrict__ stats, int8_t *__restrict__ xq8,
+                                                          float *__restrict__ xsc) {
+    constexpr int d = 256 * F4, nb = d / QK;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * BW + w;
+    const bool have = e < n_exp;
+    float4 wv[F4];
+    const float4 *w4 = (const float4 *)(W + (size_t)(have ? e : 0) * d) + lane * F4;
 #pragma unroll
-        for (int i = 0; i < F4; ++i) {
-            p[4 * i] = wv[i].x * xv[i].x;
-            p[4 * i + 1] = wv[i].y * xv[i].y;
-            p[4 * i + 2] = wv[i].z * xv[i].z;
-            p[4 * i + 3] = wv[i].w * xv[i].w;
+    for (int i = 0; i < F4; ++i) wv[i] = w4[i];
+    const int t0 = blockIdx.y * RT, t1 = min(t0 + RT, n_tok);
+    const int base0 = (blockIdx.x * BW + w) * 2, step = gridDim.x * BW * 2;
+    float4 xr[F4];
+    {
+        const float4 *x4 = (const float4 *)(x + (size_t)t0 * d) + lane * F4;
+#pragma unroll
+        for (int i = 0; i < F4; ++i) xr[i] = x4[i];
+    }
+    for (int t = t0; t < t1; ++t) {
+        const float *xt = x + (size_t)t * d;
+        float4 xv[F4];
+#pragma unroll
+        for (int i = 0; i < F4; ++i) xv[i] = xr[i];
+        {  // the next token's chunk (the last one again at the end; unused)
+            const float4 *x4 = (const float4 *)(x + (size_t)min(t + 1, t1 - 1) * d) + lane * F4;
+#pragma unroll
+            for (int i = 0; i < F4; ++i) xr[i] = x4[i];
         }
-        double c = 0.0;
-#pragma unroll
-        for (int i = 0; i < C; ++i) c += (double)p[i];
-        double incl = c;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const double n = __shfl_up(incl, o);
-            if (lane >= o) incl += n;
-        }
-        double run = __shfl_up(incl, 1);
-        if (lane == 0) run = 0.0;
-        const double total = __shfl(incl, 63);
-        double babs = 0.0;
-#pragma unroll
-        for (int i = 0; i < C; ++i) {
-            run += (double)p[i];
-            babs += fabs(run);
-        }
-        babs = wave_sum_d(babs);
-        if (lane == 0) {
-            const double u = 0x1p-24, g = u / (1.0 - u);
-            const double bound = babs * g / (1.0 - (double)d * g) * (1.0 + 0x1p-20) + 1e-300;
-            stats[(size_t)tok * n_exp + e] = make_double2(total, bound);
+        const float scale = pre_norm ? norm_x_chunk<F4>(xt, xv, eps) : 1.0f;
+        const int hb0 = base0 + (lane >> 5);
+        quant_x_blocks<F4>(xt, pre_norm, scale, base0, step, hb0 < nb ? xt[hb0 * QK + (lane & 31)] : 0.0f, nullptr,
+                           xq8 + (size_t)t * d, xsc + (size_t)t * nb, lane);
+        if (have) {
+            const double2 st = row_stats<F4>(wv, xv, lane);
+            if (lane == 0) stats[(size_t)t * n_exp + e] = st;
         }
     }
 }
@@ -216,13 +281,19 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
 
 int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, float eps, uint8_t *ws,
                   const WsLayout &lay, int32_t *ids, float *wts, float *logits, bool select) {
-    const int groups = grid_blocks(L->n_exp, RWAVES);
     const int pre = (flags & RVM_PRE_NORM) ? 1 : 0;
     return with_steps(L->d / 256, [&](auto f4) {
         constexpr int F4 = decltype(f4)::value;
-        hipLaunchKernelGGL(k_router<F4>, dim3(groups, n_tok), dim3(RWAVES * 64), 0, cur_stream(), L->router, x, L->n_exp,
-                           pre, eps, (double2 *)(ws + lay.stats), (uint32_t *)(ws + lay.xact),
-                           n_tok > 1 ? (int8_t *)(ws + lay.xq8) : nullptr, n_tok > 1 ? (float *)(ws + lay.xsc) : nullptr);
+        if (n_tok == 1) {  // decode: one wave per expert, and the prepared activation blocks
+            hipLaunchKernelGGL(k_router<F4>, dim3(grid_blocks(L->n_exp, RWAVES), 1), dim3(RWAVES * 64), 0, cur_stream(),
+                               L->router, x, L->n_exp, pre, eps, (double2 *)(ws + lay.stats),
+                               (uint32_t *)(ws + lay.xact), nullptr, nullptr);
+        } else {  // batches: about 16 token groups, so that the rows are read that many times
+            const int rt = max(1, n_tok / 16);
+            hipLaunchKernelGGL(k_router_batch<F4>, dim3(grid_blocks(L->n_exp, BW), grid_blocks(n_tok, rt)),
+                               dim3(BW * 64), 0, cur_stream(), L->router, x, n_tok, L->n_exp, rt, pre, eps,
+                               (double2 *)(ws + lay.stats), (int8_t *)(ws + lay.xq8), (float *)(ws + lay.xsc));
+        }
         int rc = launched();
         if (rc || !select) return rc;
         hipLaunchKernelGGL(k_select<F4>, dim3(n_tok), dim3(SEL_WAVES * 64), 0, cur_stream(),

@@ -128,39 +128,42 @@ __device__ __forceinline__ void wave_top_k(const uint32_t (&k)[4], bool (&alive)
     }
 }
 
-// This lane's chunk of the layer input, x or rms_norm(x) (runtime/src/ops.rs:131-139: f64 sum of
-// squares, mean as f32, 1/sqrt(mean + eps)); every wave that calls this computes the same scale.
+// rms_norm of this lane's chunk xv of the layer input xt, in place (runtime/src/ops.rs:131-139:
+// f64 sum of squares, mean as f32, 1/sqrt(mean + eps)); every wave computes the same scale.
+template <int F4>
+__device__ __forceinline__ float norm_x_chunk(const float *xt, float4 (&xv)[F4], float eps) {
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < F4; ++i)
+        s += (double)xv[i].x * (double)xv[i].x + (double)xv[i].y * (double)xv[i].y +
+             (double)xv[i].z * (double)xv[i].z + (double)xv[i].w * (double)xv[i].w;
+    s = wave_sum_d(s);  // the same value in every lane
+    // The reference sums sequentially. Both sums are within d * 2^-53 * s of the exact one, so
+    // the f32 mean is the reference's unless it sits at an f32 rounding boundary; then the sum is
+    // redone in the reference's order.
+    const double n = 256.0 * F4, bnd = s * (2.0 * n * 0x1p-53) * 1.01;
+    if ((float)((s - bnd) / n) != (float)((s + bnd) / n)) {
+        s = 0.0;
+        for (int i = 0; i < 256 * F4; ++i) {
+            const double v = (double)xt[i];
+            s += v * v;
+        }
+    }
+    const float mean = (float)(s / (double)(256 * F4));
+    const float scale = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+    for (int i = 0; i < F4; ++i)
+        xv[i] = make_float4(xv[i].x * scale, xv[i].y * scale, xv[i].z * scale, xv[i].w * scale);
+    return scale;
+}
+
+// This lane's chunk of the layer input, x or rms_norm(x): elements [4 F4 lane, 4 F4 (lane + 1)).
 template <int F4>
 __device__ __forceinline__ float load_x_chunk(const float *xt, int lane, int pre_norm, float eps, float4 (&xv)[F4]) {
     const float4 *x4 = (const float4 *)xt + lane * F4;
 #pragma unroll
     for (int i = 0; i < F4; ++i) xv[i] = x4[i];
-    float scale = 1.0f;
-    if (pre_norm) {
-        double s = 0.0;
-#pragma unroll
-        for (int i = 0; i < F4; ++i)
-            s += (double)xv[i].x * (double)xv[i].x + (double)xv[i].y * (double)xv[i].y +
-                 (double)xv[i].z * (double)xv[i].z + (double)xv[i].w * (double)xv[i].w;
-        s = wave_sum_d(s);  // the same value in every lane
-        // The reference sums sequentially. Both sums are within d * 2^-53 * s of the exact one, so
-        // the f32 mean is the reference's unless it sits at an f32 rounding boundary; then the
-        // sum is redone in the reference's order.
-        const double n = 256.0 * F4, bnd = s * (2.0 * n * 0x1p-53) * 1.01;
-        if ((float)((s - bnd) / n) != (float)((s + bnd) / n)) {
-            s = 0.0;
-            for (int i = 0; i < 256 * F4; ++i) {
-                const double v = (double)xt[i];
-                s += v * v;
-            }
-        }
-        const float mean = (float)(s / (double)(256 * F4));
-        scale = 1.0f / sqrtf(mean + eps);
-#pragma unroll
-        for (int i = 0; i < F4; ++i)
-            xv[i] = make_float4(xv[i].x * scale, xv[i].y * scale, xv[i].z * scale, xv[i].w * scale);
-    }
-    return scale;
+    return pre_norm ? norm_x_chunk<F4>(xt, xv, eps) : 1.0f;
 }
 
 // LDS of select_token for a workgroup of NW waves and d = 256 * F4.
