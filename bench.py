@@ -32,7 +32,7 @@ EXPERT_BYTES = 2816 // 32 * 18 * 1408 + 704 // 32 * 18 * 2816  # 3,345,408
 ROUTER_BYTES = 128 * 2816 * 4  # 1,441,792
 # HBM bytes one decode call moves (read + written), from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
 # this workload calibrated against a device copy of known size (profiles/decode_hbm_traffic.md).
-MEASURED_TRAFFIC = 33_696_704
+MEASURED_TRAFFIC = 33_684_001
 
 
 def log(msg: str) -> None:
