@@ -20,35 +20,29 @@ constexpr int RWAVES = 1;  // waves (experts) per router workgroup: one expert p
 constexpr int SEL_WAVES = 8;  // waves of the selecting workgroup
 
 // The logit statistics of one router row and one token: S = the f64 sum of the f32 products
-// (lane chunks summed in order, then a wave scan), and the bound on the sequential f32 fold's
+// (lane chunks summed in order, then a DPP wave scan), and the bound on the sequential f32 fold's
 // error from the prefix sums. Every lane returns the same pair.
 template <int F4>
 __device__ __forceinline__ double2 row_stats(const float4 (&wv)[F4], const float4 (&xv)[F4], int lane) {
     constexpr int d = 256 * F4, C = 4 * F4;
-    float p[C];
+    double p[C];  // the f32 products, exactly, as f64
 #pragma unroll
     for (int i = 0; i < F4; ++i) {
-        p[4 * i] = wv[i].x * xv[i].x;
-        p[4 * i + 1] = wv[i].y * xv[i].y;
-        p[4 * i + 2] = wv[i].z * xv[i].z;
-        p[4 * i + 3] = wv[i].w * xv[i].w;
+        p[4 * i] = (double)(wv[i].x * xv[i].x);
+        p[4 * i + 1] = (double)(wv[i].y * xv[i].y);
+        p[4 * i + 2] = (double)(wv[i].z * xv[i].z);
+        p[4 * i + 3] = (double)(wv[i].w * xv[i].w);
     }
     double c = 0.0;
 #pragma unroll
-    for (int i = 0; i < C; ++i) c += (double)p[i];
-    double incl = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const double n = __shfl_up(incl, o);
-        if (lane >= o) incl += n;
-    }
-    double run = __shfl_up(incl, 1);
-    if (lane == 0) run = 0.0;
-    const double total = __shfl(incl, 63);
+    for (int i = 0; i < C; ++i) c += p[i];
+    const double incl = wave_scan_d(c);
+    double run = dpp_zero_d<0x138>(incl);  // wave_shr:1: the sum of the lanes below
+    const double total = readlane_d(incl, 63);
     double babs = 0.0;
 #pragma unroll
     for (int i = 0; i < C; ++i) {
-        run += (double)p[i];
+        run += p[i];
         babs += fabs(run);
     }
     babs = wave_sum_d(babs);
@@ -81,37 +75,41 @@ __device__ __forceinline__ void quant_x_blocks(const float *__restrict__ xt, int
     }
 }
 
-// One token (blockIdx.y), one expert per wave. F4 = d / 256: lane l owns elements
-// [4 F4 l, 4 F4 (l + 1)) of a router row.
+// Decode router: one token. Workgroups 0 .. n_exp/RWAVES - 1 hold one expert per wave and form
+// its statistics; the next nb/2 workgroups quantise the token, two Q8_0 blocks each (one per
+// half-wave), so that every statistics workgroup does the same work. F4 = d / 256: lane l owns
+// elements [4 F4 l, 4 F4 (l + 1)) of a router row.
 template <int F4>
 __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict__ W, const float *__restrict__ x, int n_exp,
                                                 int pre_norm, float eps, double2 *__restrict__ stats,
-                                                uint32_t *__restrict__ xact, int8_t *__restrict__ xq8,
-                                                float *__restrict__ xsc) {
+                                                uint32_t *__restrict__ xact) {
     constexpr int d = 256 * F4, nb = d / QK;
-    const int tok = blockIdx.y;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const float *xt = x + (size_t)tok * d;
+    const int groups = (n_exp + RWAVES - 1) / RWAVES;
+    if ((int)blockIdx.x >= groups) {
+        const int base0 = ((int)blockIdx.x - groups) * RWAVES * 2 + w * 2;
+        const int hb0 = base0 + (lane >> 5);
+        const float first = hb0 < nb ? x[hb0 * QK + (lane & 31)] : 0.0f;
+        float scale = 1.0f;
+        if (pre_norm) {
+            float4 xv[F4];
+            scale = load_x_chunk<F4>(x, lane, pre_norm, eps, xv);
+        }
+        quant_x_blocks<F4>(x, pre_norm, scale, base0, nb, first, xact, nullptr, nullptr, lane);
+        return;
+    }
     const int e = blockIdx.x * RWAVES + w;
     const bool have = e < n_exp;
-
-    // All loads first: the row chunk, the x chunk, and this lane's quantisation element.
     float4 wv[F4];
     const float4 *w4 = (const float4 *)(W + (size_t)(have ? e : 0) * d) + lane * F4;
 #pragma unroll
     for (int i = 0; i < F4; ++i) wv[i] = w4[i];
-    const int base0 = (blockIdx.x * RWAVES + w) * 2;
-    const int hb0 = base0 + (lane >> 5);
-    const float qv0 = hb0 < nb ? xt[hb0 * QK + (lane & 31)] : 0.0f;
     float4 xv[F4];
-    const float scale = load_x_chunk<F4>(xt, lane, pre_norm, eps, xv);
-    // the quantisation runs while the row loads are in flight
-    quant_x_blocks<F4>(xt, pre_norm, scale, base0, gridDim.x * RWAVES * 2, qv0, xact + (size_t)tok * nb * ACT_DW,
-                       xq8 ? xq8 + (size_t)tok * d : nullptr, xq8 ? xsc + (size_t)tok * nb : nullptr, lane);
+    load_x_chunk<F4>(x, lane, pre_norm, eps, xv);
     if (have) {
         const double2 st = row_stats<F4>(wv, xv, lane);
-        if (lane == 0) stats[(size_t)tok * n_exp + e] = st;
+        if (lane == 0) stats[e] = st;
     }
 }
 
@@ -285,9 +283,9 @@ int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, floa
     return with_steps(L->d / 256, [&](auto f4) {
         constexpr int F4 = decltype(f4)::value;
         if (n_tok == 1) {  // decode: one wave per expert, and the prepared activation blocks
-            hipLaunchKernelGGL(k_router<F4>, dim3(grid_blocks(L->n_exp, RWAVES), 1), dim3(RWAVES * 64), 0, cur_stream(),
-                               L->router, x, L->n_exp, pre, eps, (double2 *)(ws + lay.stats),
-                               (uint32_t *)(ws + lay.xact), nullptr, nullptr);
+            const int groups = grid_blocks(L->n_exp, RWAVES), qgroups = grid_blocks(L->d / QK, 2 * RWAVES);
+            hipLaunchKernelGGL(k_router<F4>, dim3(groups + qgroups), dim3(RWAVES * 64), 0, cur_stream(), L->router, x,
+                               L->n_exp, pre, eps, (double2 *)(ws + lay.stats), (uint32_t *)(ws + lay.xact));
         } else {  // batches: about 16 token groups, so that the rows are read that many times
             const int rt = max(1, n_tok / 16);
             hipLaunchKernelGGL(k_router_batch<F4>, dim3(grid_blocks(L->n_exp, BW), grid_blocks(n_tok, rt)),

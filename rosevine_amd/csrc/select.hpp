@@ -33,6 +33,27 @@ __device__ __forceinline__ double readlane_d(double v, int l) {
     const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
     return __builtin_bit_cast(double, (hi << 32) | lo);
 }
+// v moved by DPP control CTRL in the rows of ROW_MASK; lanes of other rows, and lanes whose
+// source lies outside their row, read 0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double dpp_zero_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROW_MASK, 0xf, true);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROW_MASK, 0xf, true);
+    return __builtin_bit_cast(double, (hi << 32) | lo);
+}
+// Inclusive prefix sum over the 64 lanes (all active), by DPP only: row_shr 1, 2, 4, 8 within
+// each row of 16, then row_bcast:15 (row r's last lane into row r + 1, for rows 1 and 3) and
+// row_bcast:31 (lane 31 into rows 2 and 3).
+__device__ __forceinline__ double wave_scan_d(double v) {
+    v += dpp_zero_d<0x111>(v);
+    v += dpp_zero_d<0x112>(v);
+    v += dpp_zero_d<0x114>(v);
+    v += dpp_zero_d<0x118>(v);
+    v += dpp_zero_d<0x142, 0xa>(v);
+    v += dpp_zero_d<0x143, 0xc>(v);
+    return v;
+}
 // Sum over the wave (all lanes active): quads, octets and rows of 16 by DPP (each step adds the
 // same two values in every lane, so all lanes agree), then the four rows. Wave-uniform result.
 __device__ __forceinline__ double wave_sum_d(double v) {
