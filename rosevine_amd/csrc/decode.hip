@@ -166,6 +166,11 @@ __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
     __shared__ uint4 hprep[3];
     __shared__ int fix_e[MAX_TOPK];
     __shared__ int n_fix;
+    // Every argument into scalar registers before the first load is issued: the compiler would
+    // otherwise fetch part of them after it, a second round trip on the selection's path.
+    asm volatile("" ::"s"(nib), "s"(scl), "s"(dnib), "s"(dscl), "s"(stats), "s"(bias), "s"(W), "s"(x), "s"(n_exp),
+                 "s"(top_k), "s"(pre_norm), "s"(eps), "s"(exact), "s"(ctl), "s"(ids), "s"(wts), "s"(xact), "s"(hact),
+                 "s"(dterm), "s"(T));
     const int lane = threadIdx.x & 63;
     St st;
     st.load(xact, S * 3);  // in flight during the selection
