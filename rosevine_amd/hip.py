@@ -17,7 +17,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "librvmoe.so")
+# RVM_LIB names another build of the same library (for side-by-side timing of two builds)
+LIB_PATH = os.environ.get("RVM_LIB", os.path.join(HERE, "librvmoe.so"))
 
 QK, Q4_BLOCK, Q8_BLOCK = 32, 18, 34
 PACK_GATE_UP, PACK_ROWS32 = 1, 2
