@@ -127,6 +127,57 @@ def other_workload(args) -> int:
                                   "frac": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
                                   "bytes_per_step": nbytes, "int8_tops": round(ops / (ms / 1e3) / 1e12, 2),
                                   "int8_frac_of_5000_tops": round(ops / (ms / 1e3) / 5.0e15, 5)}})
+    elif args.workload == "q4gemv":
+        # the dense Q4_0 projections of one sliding-window layer of the reference model
+        # (contract.rs:41-62) and its 262,144-row output head, one token, rvh_q4_mm
+        shapes = [("attn_q", 4096, D), ("attn_k", 2048, D), ("attn_v", 2048, D), ("attn_output", D, 4096),
+                  ("ffn_gate", 2112, D), ("ffn_up", 2112, D), ("ffn_down", D, 2112)]
+        head = ("head", 262144, D)
+        rng = np.random.default_rng(args.seed)
+        mats = {}
+        for name, n_out, k in shapes + [head]:
+            wbuf = hip.DevBuf(n_out * (k // 32) * 18)
+            hip.synth_q4(wbuf, 1, n_out, k, args.seed, 1000 + len(mats))
+            mats[name] = (wbuf, hip.DevBuf.from_array(rng.standard_normal(k).astype(np.float32)),
+                          hip.DevBuf(n_out * 4), n_out, k)
+        hip.sync()
+        reps = 200
+
+        def timed(names) -> float:
+            hip.Graph.begin()
+            for _ in range(reps):
+                for nm in names:
+                    wb, xb, yb, n_out, k = mats[nm]
+                    hip.q4_mm(wb, xb, yb, n_out, k, 1)
+            g = hip.Graph.end()
+            g.launch()
+            hip.sync()
+            e0, e1 = hip.Event(), hip.Event()
+            e0.record()
+            g.launch()
+            e1.record()
+            e1.synchronize()
+            g.close()
+            return e0.elapsed_ms(e1) / reps
+
+        per = {}
+        for name, n_out, k in shapes + [head]:
+            ms1 = timed([name])
+            per[name] = {"rows": n_out, "k": k, "us": round(ms1 * 1e3, 3),
+                         "gb_s": round(n_out * (k // 32) * 18 / (ms1 / 1e3) / 1e9, 1)}
+        layer_names = [nm for nm, _, _ in shapes]
+        ms = timed(layer_names)
+        nbytes = sum(n_out * (k // 32) * 18 for _, n_out, k in shapes)
+        achieved = nbytes / (ms / 1e3) / 1e9
+        line.update({"metric": "dense Q4_0 GEMV GB/s, one layer's projections, batch 1", "value": round(achieved, 1),
+                     "unit": "GB/s", "steps": reps, "warmup": reps, "ms_per_step": round(ms, 6),
+                     "dtype": "int4 weights x f32 activations -> f32",
+                     "data": "synthetic (seeded Q4_0 weights, N(0,1) activations)", "scaling": "weak",
+                     "config": {"workload": "q4gemv", "shapes": per,
+                                "reference_gb_s": {"attn": 173, "attn_out": 204, "mlp": 154, "head": 514}},
+                     "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                                  "bytes_per_step": nbytes}})
     else:  # stack30
         L = 30
         layers = []
@@ -185,10 +236,11 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--workload", default="decode", choices=["decode", "prefill512", "ragged32", "stack30"],
+    ap.add_argument("--workload", default="decode", choices=["decode", "prefill512", "ragged32", "stack30", "q4gemv"],
                     help="decode (default, the headline line); prefill512: one layer over 512 tokens; ragged32: "
                          "one step of 32 concurrent sequences with Zipf(1.1) popularity; stack30: single-token "
-                         "decode through 30 layers with router bias and RMSNorm between layers")
+                         "decode through 30 layers with router bias and RMSNorm between layers; q4gemv: the dense "
+                         "Q4_0 projections of one layer and the output head (rvh_q4_mm), one token")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only copy this many bytes device-to-device 5 times (the calibration of the HBM "
                          "byte counters) and exit")

@@ -49,45 +49,121 @@ __global__ __launch_bounds__(256) void k_f32_mm(const float *__restrict__ w, con
     if (lane == 0) y[(size_t)t * n_out + r] = s;
 }
 
-// Q4_0 rows (reference layout) x f32 activations: one wave per row, lanes over blocks, up to
-// 8 tokens per pass; each element dequantised as ((q - 8) as f32) * d, as ops.rs:83-92.
-constexpr int QTT = 8;
+// Q4_0 rows in the reference layout (18-byte blocks: f16 d, 16 nibble bytes; runtime/src/ops.rs:83-92)
+// times f32 activations, the dense GEMV/GEMM family behind rvh_q4_mm (runtime/hip/rvhip.hip; the
+// reference's k_q4_mm). Wave w takes rows QRW w .. QRW w + QRW-1 (1 to 8, so that there are about
+// 2048 waves) and lane l block columns l, l + 64, ...: each row's blocks are read as
+// one contiguous run per wave (a 16-byte nibble load per lane, at the block's 2-byte alignment), and
+// a lane's activation block is loaded once for the wave's rows.
+// A block adds d * (sum_j n_j x_j - 8 sum_j x_j) with n_j the unsigned nibbles (one byte convert
+// and one fused multiply-add per element), which is sum_j ((n_j - 8) d) x_j up to rounding; the
+// reference's CPU ops are the tolerance target (runtime/tests/hip_ops.rs:56-81). Each output is
+// summed in a fixed order (blocks per lane in column order, then a fixed wave reduction), so a
+// token's result does not depend on the other tokens of the call.
+constexpr int QTT = 8;  // tokens per pass (calls with one token use a one-token variant)
+struct __attribute__((packed, aligned(2))) Q4Nibbles {
+    uint32_t q[4];
+};
+
+// a & m, opaque to the optimiser: the byte conversions below then map to v_cvt_f32_ubyte0..3
+// of the result, one instruction each, where knowing the bytes are nibbles makes the compiler
+// extract each one first.
+__device__ __forceinline__ uint32_t and_opaque(uint32_t a, uint32_t m) {
+    uint32_t r;
+    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(m));
+    return r;
+}
+
+// Sum over the wave in a fixed order: rows of 16 by DPP, then the four rows.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += __builtin_bit_cast(float, dpp<0xb1>(__builtin_bit_cast(uint32_t, v)));
+    v += __builtin_bit_cast(float, dpp<0x4e>(__builtin_bit_cast(uint32_t, v)));
+    v += __builtin_bit_cast(float, dpp<0x141>(__builtin_bit_cast(uint32_t, v)));
+    v += __builtin_bit_cast(float, dpp<0x140>(__builtin_bit_cast(uint32_t, v)));
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (a + b) + (c + d);
+}
+
+template <int NCOL, int QRW, int TT>  // ceil(nb / 64) block columns per lane; rows per wave; tokens
 __global__ __launch_bounds__(256) void k_q4_mm(const uint8_t *__restrict__ w, const float *__restrict__ x,
                                                float *__restrict__ y, int n_out, int k, int n_in) {
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int t0 = blockIdx.y * QTT;
-    if (r >= n_out) return;
-    const int nb = k / QK, nt = min(QTT, n_in - t0);
-    const uint8_t *row = w + (size_t)r * nb * Q4_BLOCK;
-    float acc[QTT];
+    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * QRW, lane = threadIdx.x & 63;
+    if (r0 >= n_out) return;
+    const int t0 = blockIdx.y * TT, nt = min(TT, n_in - t0);
+    const int nb = k / QK;
+    const size_t rb = (size_t)nb * Q4_BLOCK;
+    float acc[QRW][TT];
 #pragma unroll
-    for (int i = 0; i < QTT; ++i) acc[i] = 0.0f;
-    for (int b = lane; b < nb; b += 64) {
-        const uint16_t *h = (const uint16_t *)(row + (size_t)b * Q4_BLOCK);
-        const float d = h2f(h[0]);
-        float v[QK];
+    for (int r = 0; r < QRW; ++r)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t u = h[1 + j];
-            v[2 * j] = (float)((int)(u & 15) - 8) * d;
-            v[2 * j + 1] = (float)((int)((u >> 8) & 15) - 8) * d;
-            v[16 + 2 * j] = (float)((int)((u >> 4) & 15) - 8) * d;
-            v[16 + 2 * j + 1] = (float)((int)((u >> 12) & 15) - 8) * d;
-        }
+        for (int t = 0; t < TT; ++t) acc[r][t] = 0.0f;
+    for (int cg = 0; cg < nb; cg += 64 * NCOL) {  // one pass unless k > 64 NCOL blocks
+        // the group's weight loads first: QRW rows x NCOL columns (rows and columns past the end clamped)
+        float d[NCOL][QRW];
+        uint32_t q[NCOL][QRW][4];
 #pragma unroll
-        for (int i = 0; i < QTT; ++i)
-            if (i < nt) {
-                const float *xs = x + (size_t)(t0 + i) * k + (size_t)b * QK;
-                float s = 0.0f;
+        for (int c = 0; c < NCOL; ++c)
 #pragma unroll
-                for (int j = 0; j < QK; ++j) s += v[j] * xs[j];
-                acc[i] += s;
+            for (int r = 0; r < QRW; ++r) {
+                const uint8_t *blk =
+                    w + (size_t)min(r0 + r, n_out - 1) * rb + (size_t)min(cg + lane + 64 * c, nb - 1) * Q4_BLOCK;
+                d[c][r] = h2f(*(const uint16_t *)blk);
+                const Q4Nibbles v = *(const Q4Nibbles *)(blk + 2);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) q[c][r][j] = v.q[j];
             }
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            if (t >= nt) break;
+#pragma unroll
+            for (int c = 0; c < NCOL; ++c) {
+                const int b = cg + lane + 64 * c;
+                if (b >= nb) break;
+                const float4 *xb = (const float4 *)(x + (size_t)(t0 + t) * k + (size_t)b * QK);
+                float xv[QK];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float4 v = xb[i];
+                    xv[4 * i] = v.x;
+                    xv[4 * i + 1] = v.y;
+                    xv[4 * i + 2] = v.z;
+                    xv[4 * i + 3] = v.w;
+                }
+                float xs = 0.0f;
+#pragma unroll
+                for (int i = 0; i < QK; ++i) xs += xv[i];
+#pragma unroll
+                for (int r = 0; r < QRW; ++r) {
+                    float s = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t lo = and_opaque(q[c][r][j], 0x0F0F0F0Fu);
+                        const uint32_t hi = and_opaque(q[c][r][j] >> 4, 0x0F0F0F0Fu);
+                        s = fmaf((float)(lo & 0xFF), xv[4 * j], s);
+                        s = fmaf((float)((lo >> 8) & 0xFF), xv[4 * j + 1], s);
+                        s = fmaf((float)((lo >> 16) & 0xFF), xv[4 * j + 2], s);
+                        s = fmaf((float)(lo >> 24), xv[4 * j + 3], s);
+                        s = fmaf((float)(hi & 0xFF), xv[16 + 4 * j], s);
+                        s = fmaf((float)((hi >> 8) & 0xFF), xv[16 + 4 * j + 1], s);
+                        s = fmaf((float)((hi >> 16) & 0xFF), xv[16 + 4 * j + 2], s);
+                        s = fmaf((float)(hi >> 24), xv[16 + 4 * j + 3], s);
+                    }
+                    acc[r][t] = fmaf(d[c][r], s - 8.0f * xs, acc[r][t]);
+                }
+            }
+        }
     }
 #pragma unroll
-    for (int i = 0; i < QTT; ++i) {
-        const float s = wave_sum_f(acc[i]);
-        if (i < nt && lane == 0) y[(size_t)(t0 + i) * n_out + r] = s;
+    for (int t = 0; t < TT; ++t) {
+        if (t >= nt) break;
+#pragma unroll
+        for (int r = 0; r < QRW; ++r) {
+            const float v = wave_sum_dpp(acc[r][t]);
+            if (lane == 0 && r0 + r < n_out) y[(size_t)(t0 + t) * n_out + r0 + r] = v;
+        }
     }
 }
 
@@ -143,8 +219,29 @@ int rvh_f32_mm(const float *w, const float *x, float *y, int n_out, int k, int n
 int rvh_q4_mm(const void *w, const float *x, float *y, int n_out, int k, int n_in) {
     RVM_CHECK(w && x && y && n_out > 0 && n_in > 0 && k > 0 && k % QK == 0 && ((uintptr_t)w & 1) == 0);
     RVM_CHECK(grid_blocks(n_in, QTT) <= 65535);
-    hipLaunchKernelGGL(k_q4_mm, dim3(grid_blocks(n_out, 4), grid_blocks(n_in, QTT)), dim3(256), 0, cur_stream(),
-                       (const uint8_t *)w, x, y, n_out, k, n_in);
+    // rows per wave: about 2048 waves, each with as many rows' bytes in flight as that allows
+    const int ncol = min(grid_blocks(k / QK, 64), 4);
+    const int rw = n_out >= 16384 ? 8 : (n_out >= 8192 ? 4 : (n_out >= 4096 ? 2 : 1));
+    const int tt = n_in == 1 ? 1 : QTT;
+    const dim3 grid(grid_blocks(n_out, 4 * rw), grid_blocks(n_in, tt));
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, cur_stream(), (const uint8_t *)w, x, y, n_out, k, n_in);
+    };
+    auto by_cols = [&](auto rwc, auto ttc) {
+        constexpr int RW = decltype(rwc)::value, T = decltype(ttc)::value;
+        if (ncol == 1) go(k_q4_mm<1, RW, T>);
+        else if (ncol == 2) go(k_q4_mm<2, RW, T>);
+        else if (ncol == 3) go(k_q4_mm<3, RW, T>);
+        else go(k_q4_mm<4, RW, T>);
+    };
+    auto by_rows = [&](auto ttc) {
+        if (rw == 8) by_cols(std::integral_constant<int, 8>{}, ttc);
+        else if (rw == 4) by_cols(std::integral_constant<int, 4>{}, ttc);
+        else if (rw == 2) by_cols(std::integral_constant<int, 2>{}, ttc);
+        else by_cols(std::integral_constant<int, 1>{}, ttc);
+    };
+    if (tt == 1) by_rows(std::integral_constant<int, 1>{});
+    else by_rows(std::integral_constant<int, QTT>{});
     return launched();
 }
 

@@ -174,8 +174,13 @@ def test_gelu_matches_the_host_libm_bitwise(gpu, orc):
 def test_reference_ops(gpu, orc):
     rng = np.random.default_rng(41)
     # rvh_q4_mm against ops::matmul_q4_0 (runtime/tests/hip_ops.rs:56-81): rel L2 < 1e-5, batch invariance
-    for n_out, k in [(1408, 2816), (2816, 704)]:
-        for n_in in [1, 7]:
+    # shapes of the reference model's projections (contract.rs:41-62: q/k/v, output, dense FFN),
+    # block-column counts 1 .. 4, k past one column group (9216), rows not a multiple of 4, and
+    # 1, 2, 4 and 8 rows per wave; one token runs a one-token kernel, bitwise the batched one
+    for n_out, k, tokens in [(1408, 2816, [1, 7]), (2816, 704, [1, 7]), (2048, 2816, [1, 9]),
+                             (2816, 2112, [1, 3]), (1001, 8192, [1, 2]), (300, 9216, [1, 8]),
+                             (4100, 256, [1, 2]), (9000, 256, [1, 9]), (16387, 256, [1, 3])]:
+        for n_in in tokens:
             w = rand_q4(rng, n_out, k, 0.01, 0.03)
             x = rng.uniform(-1, 1, (n_in, k)).astype(np.float32)
             want = orc.matmul_q4_0(w, k, x, n_in, n_out)
