@@ -63,6 +63,26 @@ int rvh_gather_rows(const float *src, const int32_t *idx, float *dst, int n, int
 /* out[t] = sum_j (y[pos[p]] * scale[p]) * weight[p], p = t*used + j, slot order; rvhip.h:78-80. */
 int rvh_moe_combine(const float *y, const int32_t *pos, const float *scale, const float *weight, float *out,
                     int n_tok, int used, int width);
+/* Q8_0 of the keys and values of n_tok tokens ([n_tok][n_kv][hd] f32) into ring slots
+ * (p0 + t) % cap of kc and vc ([cap][n_kv][hd/32 blocks of 34 bytes]); bit for bit the CPU
+ * quantiser runtime/src/ops.rs:95-105. rvhip.h:55-56. */
+int rvh_kv_store(const float *k, const float *v, void *kc, void *vc, int n_tok, int n_kv, int hd, int p0, int cap);
+/* Causal attention, scale 1.0, of n_tok queries at positions p0.. ([n_tok][n_head][hd]); window 0
+ * is global, else keys p > pos - window; kv head of query head h is h / (n_head / n_kv).
+ * hd % 32 == 0, hd <= 512; the longest key range must be <= max_keys and <= cap. scores is the
+ * reference's n_tok * n_head * max_keys scratch: it must be non-NULL and is left untouched (the
+ * kernel is rvh_attn_split's with one chunk). rvhip.h:57-60. */
+int rvh_attention(const float *q, const void *kc, const void *vc, float *out, float *scores, int n_tok, int n_head,
+                  int n_kv, int hd, int p0, int cap, int window, int max_keys);
+/* Split-K attention, rvh_attention's result up to summation order. Each query's keys are cut into
+ * n_chunks contiguous chunks of ceil(keys / n_chunks); n_chunks == 1 writes out (part may be
+ * NULL), else part receives [n_tok * n_head][n_chunks][hd + 2] = {max, sum, acc[hd]} for
+ * rvh_attn_combine. n_chunks <= 65535. rvhip.h:61-65. */
+int rvh_attn_split(const float *q, const void *kc, const void *vc, float *out, float *part, int n_tok, int n_head,
+                   int n_kv, int hd, int p0, int cap, int window, int n_chunks);
+/* Merge rows * n_chunks partials of rvh_attn_split into rows outputs of hd. n_chunks > 1.
+ * rvhip.h:66-67. */
+int rvh_attn_combine(const float *part, float *out, int rows, int hd, int n_chunks);
 
 /* ---- Additive MoE entry points (no counterpart symbol in rvhip.h) ---- */
 

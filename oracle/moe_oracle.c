@@ -252,6 +252,67 @@ void orc_softmax(float *x, size_t n) {
     for (size_t i = 0; i < n; ++i) x[i] *= inv;
 }
 
+/* runtime/src/ops.rs:107-118: per block d * (sequential f32 fold of q * x), folded in block order. */
+float orc_dot_q8_0(const uint8_t *row, const float *x, size_t k) {
+    float acc = 0.0f;
+    for (size_t b = 0; b < k / QK; ++b) {
+        const uint8_t *blk = row + b * Q8_BLOCK;
+        const float *xs = x + b * QK;
+        float d = orc_f16_to_f32(le16(blk));
+        float s = -0.0f;
+        for (int j = 0; j < QK; ++j) s += (float)(int8_t)blk[2 + j] * xs[j];
+        acc += d * s;
+    }
+    return acc;
+}
+
+/* runtime/src/ops.rs:120-128: out += q * (d * w), element by element. */
+void orc_axpy_q8_0(const uint8_t *row, float w, float *out, size_t k) {
+    for (size_t b = 0; b < k / QK; ++b) {
+        const uint8_t *blk = row + b * Q8_BLOCK;
+        float d = orc_f16_to_f32(le16(blk)) * w;
+        for (int j = 0; j < QK; ++j) out[b * QK + j] += (float)(int8_t)blk[2 + j] * d;
+    }
+}
+
+/* runtime/tests/hip_ops.rs:245-271 (the CPU attention the reference's kernels are checked
+ * against): query t at position p0 + t, keys lo..pos with lo = pos + 1 - win saturated at 0
+ * (win > 0) or 0, key p in ring row ((p % cap) * nkv + g) for g = h / (nh / nkv); scores
+ * dot_q8_0, softmax, then out = sum of axpy_q8_0 in key order from zero. */
+void orc_attention(const float *q, const uint8_t *kc, const uint8_t *vc, size_t nh, size_t nkv, size_t hd,
+                   size_t cap, size_t win, size_t p0, size_t n, float *out) {
+    size_t row = hd / QK * Q8_BLOCK;
+    float *sc = (float *)malloc((p0 + n) * sizeof(float));
+    memset(out, 0, n * nh * hd * sizeof(float));
+    for (size_t t = 0; t < n; ++t) {
+        size_t pos = p0 + t;
+        size_t lo = win > 0 ? (pos + 1 > win ? pos + 1 - win : 0) : 0;
+        for (size_t h = 0; h < nh; ++h) {
+            size_t g = h / (nh / nkv);
+            const float *qh = q + (t * nh + h) * hd;
+            for (size_t p = lo; p <= pos; ++p) sc[p - lo] = orc_dot_q8_0(kc + ((p % cap) * nkv + g) * row, qh, hd);
+            orc_softmax(sc, pos - lo + 1);
+            float *o = out + (t * nh + h) * hd;
+            for (size_t p = lo; p <= pos; ++p) orc_axpy_q8_0(vc + ((p % cap) * nkv + g) * row, sc[p - lo], o, hd);
+        }
+    }
+    free(sc);
+}
+
+/* runtime/tests/hip_ops.rs:9-22: the reference tests' xorshift64 generator. unit() maps the top
+ * 24 bits of each state to [-1, 1); vec(n, scale) is n of unit() * scale. */
+void orc_test_rng_vec(uint64_t *state, size_t n, float scale, float *out) {
+    uint64_t s = *state;
+    for (size_t i = 0; i < n; ++i) {
+        s ^= s << 13;
+        s ^= s >> 7;
+        s ^= s << 17;
+        float u = (float)(s >> 40) / 16777216.0f * 2.0f - 1.0f;
+        out[i] = u * scale;
+    }
+    *state = s;
+}
+
 /* Rust f32::total_cmp key (IEEE 754 totalOrder as a signed integer). */
 static int32_t total_key(float f) {
     int32_t i = (int32_t)f32_bits(f);

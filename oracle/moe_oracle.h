@@ -11,7 +11,7 @@
  * maps NaN to 0, f32::max ignores NaN (fmaxf), total_cmp is the IEEE total order, float sums
  * are sequential folds, f32::exp/tanh are the platform expf/tanhf.
  *
- * Parity pinning: tests/test_oracle.py checks every function against the reference's literal
+ * Parity pinning: tests/test_oracle.py and tests/test_oracle_attention.py check every function against the reference's literal
  * known answers, independent implementations (numpy's IEEE half conversion, float32 sequential
  * accumulate, stable sort), closed forms, f64 brute force or exhaustive sweeps;
  * tests/test_oracle_mutations.py plants plausible mistakes in a copy of this file and shows that
@@ -59,6 +59,17 @@ float orc_gelu(float x);
 void orc_geglu_split(const float *gu, float *out, size_t rows, size_t ff);
 /* runtime/src/ops.rs:170-179 */
 void orc_softmax(float *x, size_t n);
+/* runtime/src/ops.rs:107-118 */
+float orc_dot_q8_0(const uint8_t *row, const float *x, size_t k);
+/* runtime/src/ops.rs:120-128 */
+void orc_axpy_q8_0(const uint8_t *row, float w, float *out, size_t k);
+/* runtime/tests/hip_ops.rs:245-271: causal attention over a Q8_0 key/value ring, scale 1.0,
+ * window 0 = global. q, out: [n][nh][hd]; kc, vc: [cap][nkv][hd/32 blocks]. */
+void orc_attention(const float *q, const uint8_t *kc, const uint8_t *vc, size_t nh, size_t nkv, size_t hd,
+                   size_t cap, size_t win, size_t p0, size_t n, float *out);
+/* runtime/tests/hip_ops.rs:9-22: the reference tests' generator, so that tests here can feed the
+ * kernels the reference tests' own inputs. Advances *state by n draws. */
+void orc_test_rng_vec(uint64_t *state, size_t n, float scale, float *out);
 /* runtime/src/ops.rs:182-187 */
 void orc_top_k(const float *x, size_t n, size_t k, uint32_t *out);
 /* Router logits with the plain projection W_r . x (ops.rs:321-326) plus an optional per-expert

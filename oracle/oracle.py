@@ -55,6 +55,10 @@ def _declare(L):
         "orc_rms_norm": (None, [vp, vp, sz, f32, f32]),
         "orc_gelu": (f32, [f32]),
         "orc_softmax": (None, [vp, sz]),
+        "orc_dot_q8_0": (f32, [vp, vp, sz]),
+        "orc_axpy_q8_0": (None, [vp, f32, vp, sz]),
+        "orc_attention": (None, [vp, vp, vp, sz, sz, sz, sz, sz, sz, sz, vp]),
+        "orc_test_rng_vec": (None, [C.POINTER(C.c_uint64), sz, f32, vp]),
         "orc_geglu_split": (None, [vp, vp, sz, sz]),
         "orc_top_k": (None, [vp, sz, sz, vp]),
         "orc_router_logits": (None, [vp, vp, vp, sz, sz, sz, vp]),
@@ -114,6 +118,57 @@ def quantize_q8_0(x) -> np.ndarray:
     out = np.empty(x.size // QK * Q8_BLOCK, np.uint8)
     lib().orc_quantize_q8_0(_p(x), _p(out), x.size)
     return out
+
+
+class TestRng:
+    """The reference tests' xorshift64 generator (runtime/tests/hip_ops.rs:9-22)."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(seed)
+
+    def vec(self, n: int, scale: float) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        lib().orc_test_rng_vec(C.byref(self.state), n, scale, _p(out))
+        return out
+
+
+def test_q8_caches(rng: TestRng, total: int, cap: int, nkv: int, hd: int):
+    """runtime/tests/hip_ops.rs:229-241: positions 0..total-1, each kv head's key row then value row
+    drawn from rng and quantised into ring slot p % cap (later positions overwrite)."""
+    rows = rng.vec(total * nkv * 2 * hd, 1.0).reshape(total, nkv, 2, hd)
+    row = hd // QK * Q8_BLOCK
+    kc, vc = np.zeros((cap, nkv * row), np.uint8), np.zeros((cap, nkv * row), np.uint8)
+    first = max(0, total - cap)  # older positions are overwritten
+    slots = np.arange(first, total) % cap
+    kc[slots] = quantize_q8_0(rows[first:, :, 0]).reshape(-1, nkv * row)
+    vc[slots] = quantize_q8_0(rows[first:, :, 1]).reshape(-1, nkv * row)
+    return kc.reshape(-1), vc.reshape(-1)
+
+
+def dot_q8_0(row, x) -> float:
+    """runtime/src/ops.rs:107-118: a Q8_0 row times f32 x."""
+    row, x = _u8(row), _f32(x)
+    return lib().orc_dot_q8_0(_p(row), _p(x), x.size)
+
+
+def axpy_q8_0(row, w: float, out) -> np.ndarray:
+    """runtime/src/ops.rs:120-128: out += w * row, in place on a float32 array."""
+    row = _u8(row)
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    lib().orc_axpy_q8_0(_p(row), w, _p(out), out.size)
+    return out
+
+
+def attention(q, kc, vc, n_head, n_kv, hd, cap, window, p0, n_tok) -> np.ndarray:
+    """runtime/tests/hip_ops.rs:245-271: CPU attention of n_tok queries at p0.. over a Q8_0 ring."""
+    q, kc, vc = _f32(q).reshape(-1), _u8(kc).reshape(-1), _u8(vc).reshape(-1)
+    row = hd // QK * Q8_BLOCK
+    assert q.size == n_tok * n_head * hd and kc.size >= cap * n_kv * row and vc.size >= cap * n_kv * row
+    longest = min(p0 + n_tok, window) if window > 0 else p0 + n_tok
+    assert longest <= cap and n_head % n_kv == 0 and hd % QK == 0
+    out = np.empty(n_tok * n_head * hd, np.float32)
+    lib().orc_attention(_p(q), _p(kc), _p(vc), n_head, n_kv, hd, cap, window, p0, n_tok, _p(out))
+    return out.reshape(n_tok, n_head, hd)
 
 
 def dot_q8_scalar(row, xq, k) -> float:

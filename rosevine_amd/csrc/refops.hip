@@ -65,28 +65,6 @@ struct __attribute__((packed, aligned(2))) Q4Nibbles {
     uint32_t q[4];
 };
 
-// a & m, opaque to the optimiser: the byte conversions below then map to v_cvt_f32_ubyte0..3
-// of the result, one instruction each, where knowing the bytes are nibbles makes the compiler
-// extract each one first.
-__device__ __forceinline__ uint32_t and_opaque(uint32_t a, uint32_t m) {
-    uint32_t r;
-    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(m));
-    return r;
-}
-
-// Sum over the wave in a fixed order: rows of 16 by DPP, then the four rows.
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-    v += __builtin_bit_cast(float, dpp<0xb1>(__builtin_bit_cast(uint32_t, v)));
-    v += __builtin_bit_cast(float, dpp<0x4e>(__builtin_bit_cast(uint32_t, v)));
-    v += __builtin_bit_cast(float, dpp<0x141>(__builtin_bit_cast(uint32_t, v)));
-    v += __builtin_bit_cast(float, dpp<0x140>(__builtin_bit_cast(uint32_t, v)));
-    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-    return (a + b) + (c + d);
-}
-
 template <int NCOL, int QRW, int TT>  // ceil(nb / 64) block columns per lane; rows per wave; tokens
 __global__ __launch_bounds__(256) void k_q4_mm(const uint8_t *__restrict__ w, const float *__restrict__ x,
                                                float *__restrict__ y, int n_out, int k, int n_in) {

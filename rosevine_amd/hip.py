@@ -81,6 +81,10 @@ SIGNATURES = {
     "rvh_geglu_split": (_i, [_vp, _vp, _i, _i]),
     "rvh_gather_rows": (_i, [_vp, _vp, _vp, _i, _i]),
     "rvh_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
+    "rvh_kv_store": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
+    "rvh_attention": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i]),
+    "rvh_attn_split": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i]),
+    "rvh_attn_combine": (_i, [_vp, _vp, _i, _i, _i]),
     "rvm_set_stream": (_i, [_vp]),
     "rvm_stream_create": (_i, [C.POINTER(_vp)]),
     "rvm_stream_destroy": (_i, [_vp]),
@@ -350,6 +354,77 @@ def moe_combine(y: DevBuf, y_rows: int, pos: DevBuf, scale: DevBuf, weight: DevB
     pairs = n_tok * used
     check(lib().rvh_moe_combine(_need(y, y_rows * width * 4), _need(pos, pairs * 4), _need(scale, pairs * 4),
                                 _need(weight, pairs * 4), _need(out, n_tok * width * 4), n_tok, used, width))
+
+
+# ---- decode attention over a Q8_0 key/value ring (runtime/src/hip.rs:423-530) ----
+
+ATTN_TARGET_BLOCKS = 1024  # runtime/src/hip.rs:481
+ATTN_MIN_CHUNK = 64  # runtime/src/hip.rs:483
+
+
+def q8_row_bytes(hd: int) -> int:
+    return hd // QK * Q8_BLOCK
+
+
+def attention_chunks(n_tok: int, n_head: int, longest: int) -> int:
+    """Key chunks per query head (runtime/src/hip.rs:486-490): ceil(keys / 64), at most
+    1024 / (tokens * heads) so that decode fills the device and prefill takes one chunk."""
+    by_keys = max(-(-longest // ATTN_MIN_CHUNK), 1)
+    by_blocks = max(ATTN_TARGET_BLOCKS // max(n_tok * n_head, 1), 1)
+    return min(by_keys, by_blocks)
+
+
+def attention_split_scratch(n_tok: int, n_head: int, hd: int) -> int:
+    """f32 elements of partial scratch for attention_split at up to n_tok tokens, any context
+    (runtime/src/hip.rs:495-497)."""
+    return max(n_tok * n_head, ATTN_TARGET_BLOCKS) * (hd + 2)
+
+
+def _attn_longest(n_tok: int, p0: int, window: int) -> int:
+    return min(p0 + n_tok, window) if window > 0 else p0 + n_tok
+
+
+def kv_store(k: DevBuf, v: DevBuf, kc: DevBuf, vc: DevBuf, n_tok: int, n_kv: int, hd: int, p0: int, cap: int,
+             k_off: int = 0, v_off: int = 0) -> None:
+    """rvh_kv_store (runtime/src/hip.rs:423-438): Q8_0 of n_tok tokens' keys and values into slots
+    (p0 + t) % cap."""
+    n, c = n_tok * n_kv * hd * 4, cap * n_kv * q8_row_bytes(hd)
+    check(lib().rvh_kv_store(_need(k, n, k_off), _need(v, n, v_off), _need(kc, c), _need(vc, c), n_tok, n_kv, hd,
+                             p0, cap))
+
+
+def attention(q: DevBuf, kc: DevBuf, vc: DevBuf, out: DevBuf, scores: DevBuf, n_tok: int, n_head: int, n_kv: int,
+              hd: int, p0: int, cap: int, window: int, max_keys: int) -> None:
+    """rvh_attention (runtime/src/hip.rs:440-478); scores must hold n_tok * n_head * max_keys floats."""
+    nq, c = n_tok * n_head * hd * 4, cap * n_kv * q8_row_bytes(hd)
+    check(lib().rvh_attention(_need(q, nq), _need(kc, c), _need(vc, c), _need(out, nq),
+                              _need(scores, n_tok * n_head * max_keys * 4), n_tok, n_head, n_kv, hd, p0, cap,
+                              window, max_keys))
+
+
+def attn_split(q: DevBuf, kc: DevBuf, vc: DevBuf, out: DevBuf, part: DevBuf | None, n_tok: int, n_head: int,
+               n_kv: int, hd: int, p0: int, cap: int, window: int, n_chunks: int) -> None:
+    """rvh_attn_split with an explicit chunk count."""
+    nq, c = n_tok * n_head * hd * 4, cap * n_kv * q8_row_bytes(hd)
+    pp = _need(part, n_tok * n_head * n_chunks * (hd + 2) * 4) if n_chunks > 1 else (part.at() if part else None)
+    check(lib().rvh_attn_split(_need(q, nq), _need(kc, c), _need(vc, c), _need(out, nq), pp, n_tok, n_head, n_kv,
+                               hd, p0, cap, window, n_chunks))
+
+
+def attn_combine(part: DevBuf, out: DevBuf, rows: int, hd: int, n_chunks: int) -> None:
+    check(lib().rvh_attn_combine(_need(part, rows * n_chunks * (hd + 2) * 4), _need(out, rows * hd * 4), rows, hd,
+                                 n_chunks))
+
+
+def attention_split(q: DevBuf, kc: DevBuf, vc: DevBuf, out: DevBuf, part: DevBuf, n_tok: int, n_head: int, n_kv: int,
+                    hd: int, p0: int, cap: int, window: int) -> int:
+    """Split-K attention as runtime/src/hip.rs:503-530: attention_chunks chunks per query head, the
+    partials merged by rvh_attn_combine when there is more than one. Returns the chunk count."""
+    chunks = attention_chunks(n_tok, n_head, _attn_longest(n_tok, p0, window))
+    attn_split(q, kc, vc, out, part, n_tok, n_head, n_kv, hd, p0, cap, window, chunks)
+    if chunks > 1:
+        attn_combine(part, out, n_tok * n_head, hd, chunks)
+    return chunks
 
 
 def moe_plan(ids: DevBuf, n_pairs: int, n_exp: int, order: DevBuf, pos_of: DevBuf, group_start: DevBuf) -> None:

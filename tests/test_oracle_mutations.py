@@ -17,6 +17,7 @@ import sys
 import pytest
 
 import test_oracle as T
+import test_oracle_attention as TA
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE = os.path.join(os.path.dirname(HERE), "oracle")
@@ -97,6 +98,26 @@ MUTATIONS = [
      "for (size_t i = 0; i < d; ++i) o[i] += yy[i] * ds * wt;",
      "for (size_t i = 0; i < d; ++i) o[i] += yy[i] * (ds * wt);",
      [T.test_experts_q8_against_f64_pipeline]),
+    ("Q8 f32 dot reads the quants unsigned",
+     "s += (float)(int8_t)blk[2 + j] * xs[j];",
+     "s += (float)blk[2 + j] * xs[j];",
+     [TA.test_q8_dot_exact_cases, TA.test_q8_dot_and_axpy_against_f64]),
+    ("Q8 axpy drops the weight",
+     "float d = orc_f16_to_f32(le16(blk)) * w;",
+     "float d = orc_f16_to_f32(le16(blk));",
+     [TA.test_q8_dot_and_axpy_reference_known_answers, TA.test_q8_dot_and_axpy_against_f64]),
+    ("attention window one key too wide",
+     "(pos + 1 > win ? pos + 1 - win : 0)",
+     "(pos + 1 > win ? pos - win : 0)",
+     [TA.test_attention_against_exact_f64, TA.test_attention_fixed_cases]),
+    ("attention maps query heads to kv heads round-robin",
+     "size_t g = h / (nh / nkv);",
+     "size_t g = h % nkv;",
+     [TA.test_attention_against_exact_f64, TA.test_attention_window_heads_and_ring_invariance]),
+    ("attention reads the ring at the position, not its slot",
+     "sc[p - lo] = orc_dot_q8_0(kc + ((p % cap) * nkv + g) * row, qh, hd);",
+     "sc[p - lo] = orc_dot_q8_0(kc + ((p % (cap + 1) % cap) * nkv + g) * row, qh, hd);",
+     [TA.test_attention_against_exact_f64]),
 ]
 
 
