@@ -178,6 +178,85 @@ def other_workload(args) -> int:
                      "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                                   "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                                   "bytes_per_step": nbytes}})
+    elif args.workload == "attn":
+        # one decode token's attention through the reference model's 30 layers at depth 16384
+        # (5 global: 16 heads, 2 kv heads, hd 512; 25 sliding-window: 16 heads, 8 kv heads, hd 256,
+        # window 1024): per layer the new key/value row is quantised into the ring (rvh_kv_store),
+        # then split-K attention with the reference's chunk policy and its merge
+        depth = 16384
+        cfgs = {"global": (16, 2, 512, 0, depth + 1), "local": (16, 8, 256, 1024, 1028)}
+        kinds = ["global" if (l % 6) == 5 else "local" for l in range(30)]
+        rng = np.random.default_rng(args.seed)
+        layers = []
+        for kind in kinds:
+            nh, nkv, hd, win, cap = cfgs[kind]
+            row = hd // 32 * 34
+            rings = []
+            for _ in range(2):
+                blk = rng.integers(0, 256, (cap * nkv * (hd // 32), 34), dtype=np.uint8)
+                blk[:, :2] = (rng.uniform(0.005, 0.02, cap * nkv * (hd // 32)).astype(np.float16)
+                              .view(np.uint8).reshape(-1, 2))
+                rings.append(hip.DevBuf.from_array(blk.reshape(-1)))
+            kv_new = hip.DevBuf.from_array(rng.standard_normal(2 * nkv * hd).astype(np.float32))
+            q = hip.DevBuf.from_array((rng.standard_normal(nh * hd) * 0.2).astype(np.float32))
+            layers.append((kind, nh, nkv, hd, win, cap, rings[0], rings[1], kv_new, q, hip.DevBuf(nh * hd * 4),
+                           hip.DevBuf(hip.attention_split_scratch(1, nh, hd) * 4)))
+        hip.sync()
+        p0 = depth  # the token at position 16384 attends to 16385 keys (global) or 1024 (local)
+
+        def one_token(sel):
+            for kind, nh, nkv, hd, win, cap, kc, vc, kv_new, q, out, part in layers:
+                if sel and kind != sel:
+                    continue
+                hip.kv_store(kv_new, kv_new, kc, vc, 1, nkv, hd, p0, cap, v_off=nkv * hd * 4)
+                hip.attention_split(q, kc, vc, out, part, 1, nh, nkv, hd, p0, cap, win)
+
+        reps = 50
+        one_token(None)  # eager once: the launcher's per-kernel occupancy queries happen outside capture
+        hip.sync()
+
+        def timed(sel) -> float:
+            hip.Graph.begin()
+            for _ in range(reps):
+                one_token(sel)
+            g = hip.Graph.end()
+            g.launch()
+            hip.sync()
+            e0, e1 = hip.Event(), hip.Event()
+            e0.record()
+            g.launch()
+            e1.record()
+            e1.synchronize()
+            g.close()
+            return e0.elapsed_ms(e1) / reps
+
+        def kv_bytes(kind):
+            nh, nkv, hd, win, cap = cfgs[kind]
+            keys = min(p0 + 1, win) if win else p0 + 1
+            return keys * nkv * (hd // 32 * 34) * 2
+
+        per = {}
+        for kind in ("global", "local"):
+            n = kinds.count(kind)
+            ms_k = timed(kind)
+            per[kind] = {"layers": n, "us_per_layer": round(ms_k * 1e3 / n, 2),
+                         "kv_bytes_per_layer": kv_bytes(kind),
+                         "gb_s": round(kv_bytes(kind) * n / (ms_k / 1e3) / 1e9, 1)}
+        ms = timed(None)
+        nbytes = sum(kv_bytes(k) for k in kinds)
+        achieved = nbytes / (ms / 1e3) / 1e9
+        line.update({"metric": "decode attention (attn_core: KV store + split-K attention), 30 layers, depth 16384, "
+                               "batch 1: per-token time and K+V GB/s",
+                     "value": round(achieved, 1), "unit": "GB/s", "higher_is_better": True, "steps": reps,
+                     "warmup": reps, "ms_per_step": round(ms, 6), "dtype": "Q8_0 K/V x f32 q -> f32 (bf16x3 MFMA scores)",
+                     "data": "synthetic (random Q8_0 rings, N(0,0.2) queries)", "scaling": "weak",
+                     "config": {"workload": "attn", "depth": depth, "layers": per,
+                                "reference_attn_core_ms": {"d16384": 7.8, "global_part": 5.7,
+                                                           "note": "reference host GPU, sync mode "
+                                                                   "(docs/split-k-attention.md:75)"}},
+                     "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                                  "bytes_per_step": nbytes}})
     else:  # stack30
         L = 30
         layers = []
@@ -236,11 +315,13 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--workload", default="decode", choices=["decode", "prefill512", "ragged32", "stack30", "q4gemv"],
+    ap.add_argument("--workload", default="decode", choices=["decode", "prefill512", "ragged32", "stack30", "q4gemv", "attn"],
                     help="decode (default, the headline line); prefill512: one layer over 512 tokens; ragged32: "
                          "one step of 32 concurrent sequences with Zipf(1.1) popularity; stack30: single-token "
                          "decode through 30 layers with router bias and RMSNorm between layers; q4gemv: the dense "
-                         "Q4_0 projections of one layer and the output head (rvh_q4_mm), one token")
+                         "Q4_0 projections of one layer and the output head (rvh_q4_mm), one token; attn: one "
+                         "decode token's attention (KV store, split-K attention, merge) through 30 layers at depth "
+                         "16384")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only copy this many bytes device-to-device 5 times (the calibration of the HBM "
                          "byte counters) and exit")
