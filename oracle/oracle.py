@@ -20,9 +20,46 @@ QK, Q4_BLOCK, Q8_BLOCK = 32, 18, 34
 _lib = None
 
 
+REF_SRC = "/root/reference/runtime/hip/rvhip.hip"
+REF_LIB_PATH = os.path.join(HERE, "_ref", "librvhip_ref.so")
+
+
 def build() -> None:
-    """Compile the oracle with its Makefile (gcc, -ffp-contract=off)."""
+    """Compile the oracle with its Makefile (gcc, -ffp-contract=off), and the reference's own HIP
+    kernels into _ref/ when the reference tree is present (it is not on the GPU box, which uses
+    the library built here)."""
     subprocess.run(["make", "-s", "-B", "-C", HERE, "liboracle.so"], check=True)
+    if os.path.exists(REF_SRC):
+        subprocess.run(["make", "-s", "-B", "-C", HERE, "_ref/librvhip_ref.so"], check=True)
+
+
+def ref_lib():
+    """The reference's HIP kernels (runtime/hip/rvhip.hip) built by oracle/Makefile, or None when
+    they were not built. Loaded with local symbol binding: the product library exports the same
+    rvh_* names, and each handle resolves to its own."""
+    if not os.path.exists(REF_LIB_PATH):
+        return None
+    L = C.CDLL(REF_LIB_PATH, mode=os.RTLD_LOCAL | os.RTLD_NOW)
+    vp, i, f = C.c_void_p, C.c_int, C.c_float
+    sig = {
+        "rvh_init": [i],
+        "rvh_sync": [],
+        "rvh_kv_store": [vp, vp, vp, vp, i, i, i, i, i],
+        "rvh_attention": [vp, vp, vp, vp, vp, i, i, i, i, i, i, i, i],
+        "rvh_attn_split": [vp, vp, vp, vp, vp, i, i, i, i, i, i, i, i],
+        "rvh_attn_combine": [vp, vp, i, i, i],
+        "rvh_q4_mm": [vp, vp, vp, i, i, i],
+        "rvh_rms_norm": [vp, vp, vp, i, i, f, f],
+        "rvh_f32_mm": [vp, vp, vp, i, i, i],
+        "rvh_geglu_split": [vp, vp, i, i],
+        "rvh_gather_rows": [vp, vp, vp, i, i],
+        "rvh_moe_combine": [vp, vp, vp, vp, vp, i, i, i],
+    }
+    for name, args in sig.items():
+        fn = getattr(L, name)
+        fn.restype = i
+        fn.argtypes = args
+    return L
 
 
 def lib() -> C.CDLL:
