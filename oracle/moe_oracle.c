@@ -1,5 +1,5 @@
 /* moe_oracle.c - CPU restatement of the reference's quantized MoE expert path.
- * TEST INFRASTRUCTURE ONLY (the checker); see moe_oracle.h for the rules it follows.
+ * TEST INFRASTRUCTURE ONLY; see moe_oracle.h for the rules it follows.
  * Compile with -ffp-contract=off: every multiply and add below rounds on its own. */
 #include "moe_oracle.h"
 

@@ -1,9 +1,9 @@
 /* moe_oracle.h - CPU restatement of the reference's quantized MoE expert path.
  *
- * TEST INFRASTRUCTURE ONLY. This oracle is the checker for the HIP path: only tests/,
+ * TEST INFRASTRUCTURE ONLY. The HIP path is compared with this oracle: only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg load it. The product library
  * (rosevine_amd/librvmoe.so) never links, loads or calls it. oracle/Makefile also builds the
- * reference's own HIP kernels into oracle/_ref/ (a second checker for the GPU tests).
+ * reference's own HIP kernels into oracle/_ref/ (a second reference for the GPU tests).
  *
  * Every function restates the reference's Rust (paths relative to the reference root) in
  * the same operation order, compiled with -ffp-contract=off so that no multiply-add is fused,

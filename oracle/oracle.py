@@ -1,6 +1,6 @@
 """ctypes view of the CPU oracle (oracle/liboracle.so).
 
-TEST INFRASTRUCTURE ONLY: the checker for the HIP path. Only tests/, __graft_entry__.smoke()
+TEST INFRASTRUCTURE ONLY: what the HIP path is compared with. Only tests/, __graft_entry__.smoke()
 and bench.py's cpu_baseline leg import this module; the product (rosevine_amd) never does.
 Each wrapper names the reference function its C routine restates (moe_oracle.h).
 """
@@ -26,8 +26,8 @@ REF_LIB_PATH = os.path.join(HERE, "_ref", "librvhip_ref.so")
 
 def build() -> None:
     """Compile the oracle with its Makefile (gcc, -ffp-contract=off), and the reference's own HIP
-    kernels into _ref/ when the reference tree is present (it is not on the GPU box, which uses
-    the library built here)."""
+    kernels into _ref/ when the reference tree is present (where it is absent, a library built
+    earlier is used)."""
     subprocess.run(["make", "-s", "-B", "-C", HERE, "liboracle.so"], check=True)
     if os.path.exists(REF_SRC):
         subprocess.run(["make", "-s", "-B", "-C", HERE, "_ref/librvhip_ref.so"], check=True)

@@ -7,10 +7,12 @@
 //      by the statistics itself (select.hpp) and streams one 64-row tile (32 gate rows and the
 //      matching 32 up rows) of its slot's expert with the K range split over 8 waves, folds each
 //      row's block terms in block order, applies GeGLU and quantises the 32 h values to one Q8_0
-//      block. Workgroup 0 certifies that ranking, or computes the exact selection when it cannot
-//      be certified, publishes ids and weights, and computes any expert the ranking missed;
-//   3. k_down_decode: d/32 workgroups of 8 waves; wave j streams slot j's 32-row down tile (two
-//      half-waves split K) and wave 0 combines the 8 results in slot order.
+//      block t of h; with the down entries of block t of every down row of the same expert (loaded
+//      with the gate/up entries), it then writes the down terms of that h block for all d rows.
+//      Workgroup 0 certifies that ranking, or computes the exact selection when it cannot be
+//      certified, publishes ids and weights, and computes any expert the ranking missed;
+//   3. k_down_fold: d/32 workgroups; each folds the ff/32 down terms of its 32 rows for every slot
+//      in block order and combines the slots in slot order.
 // Every lane issues all of its 16-byte weight loads before the first use, the activation blocks
 // are staged once per workgroup in LDS, and each wave reads its blocks from LDS in one burst.
 #include "select.hpp"

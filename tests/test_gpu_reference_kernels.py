@@ -1,14 +1,13 @@
 """The reference's own HIP kernels (runtime/hip/rvhip.hip, built into oracle/_ref by
-oracle/Makefile) as a second checker, on the same device buffers and the reference tests' inputs.
+oracle/Makefile) as a second reference, on the same device buffers and the reference tests' inputs.
 
-For each operator whose reference is a HIP kernel, this build's entry point is compared with the
+For each operator whose reference is a HIP kernel, the library's entry point is compared with the
 reference's at the bar the reference sets between its own implementations: bit for bit where it
 asserts that (the key/value store, gather, the slot-order combine), relative L2 < 1e-5 where it
 compares kernels of different summation order (attention: runtime/tests/hip_ops.rs:273-310; the
 Q4_0 GEMV: hip_ops.rs:56-81), and 1e-6 for the elementwise and f32 helpers (hip_ops.rs:402-420).
 Skipped when the reference kernels were not built (no reference tree at build time).
 """
-import ctypes as C
 
 import numpy as np
 import pytest
@@ -64,7 +63,7 @@ def test_kv_store_bit_for_bit_with_the_reference_kernel(gpu, ref, orc):
 
 
 def test_attention_against_the_reference_kernels(gpu, ref, orc):
-    # runtime/tests/hip_ops.rs:273-310 with its inputs: this build's split attention (with the
+    # runtime/tests/hip_ops.rs:273-310 with its inputs: the library's split attention (with the
     # reference's chunk policy) against the reference's split kernel at the same chunk count and
     # against its one-pass kernel
     r = orc.TestRng(5)

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/moe_oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/moe_oracle.c) before the GPU tests compare the HIP path with it.
 
 Each check comes from outside the oracle's own formula: the reference's literal known answers
 (runtime/src/ops.rs:358-447, runtime/src/expert_kernel.rs:261-401,
