@@ -187,6 +187,7 @@ def other_workload(args) -> int:
         cfgs = {"global": (16, 2, 512, 0, depth + 1), "local": (16, 8, 256, 1024, 1028)}
         kinds = ["global" if (l % 6) == 5 else "local" for l in range(30)]
         rng = np.random.default_rng(args.seed)
+        target = hip.ATTN_TARGET_BLOCKS_MI355X  # the reference's chunk policy, MI355X's target
         layers = []
         for kind in kinds:
             nh, nkv, hd, win, cap = cfgs[kind]
@@ -200,7 +201,7 @@ def other_workload(args) -> int:
             kv_new = hip.DevBuf.from_array(rng.standard_normal(2 * nkv * hd).astype(np.float32))
             q = hip.DevBuf.from_array((rng.standard_normal(nh * hd) * 0.2).astype(np.float32))
             layers.append((kind, nh, nkv, hd, win, cap, rings[0], rings[1], kv_new, q, hip.DevBuf(nh * hd * 4),
-                           hip.DevBuf(hip.attention_split_scratch(1, nh, hd) * 4)))
+                           hip.DevBuf(hip.attention_split_scratch(1, nh, hd, target) * 4)))
         hip.sync()
         p0 = depth  # the token at position 16384 attends to 16385 keys (global) or 1024 (local)
 
@@ -209,7 +210,7 @@ def other_workload(args) -> int:
                 if sel and kind != sel:
                     continue
                 hip.kv_store(kv_new, kv_new, kc, vc, 1, nkv, hd, p0, cap, v_off=nkv * hd * 4)
-                hip.attention_split(q, kc, vc, out, part, 1, nh, nkv, hd, p0, cap, win)
+                hip.attention_split(q, kc, vc, out, part, 1, nh, nkv, hd, p0, cap, win, target)
 
         reps = 50
         one_token(None)  # eager once: the launcher's per-kernel occupancy queries happen outside capture
@@ -251,6 +252,7 @@ def other_workload(args) -> int:
                      "warmup": reps, "ms_per_step": round(ms, 6), "dtype": "Q8_0 K/V x f32 q -> f32 (bf16x3 MFMA scores)",
                      "data": "synthetic (random Q8_0 rings, N(0,0.2) queries)", "scaling": "weak",
                      "config": {"workload": "attn", "depth": depth, "layers": per,
+                                "chunk_policy": f"runtime/src/hip.rs:486-490 with target {target} (the reference's 1024)",
                                 "reference_attn_core_ms": {"d16384": 7.8, "global_part": 5.7,
                                                            "note": "reference host GPU, sync mode "
                                                                    "(docs/split-k-attention.md:75)"}},
