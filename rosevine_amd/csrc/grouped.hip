@@ -4,7 +4,10 @@
 //
 //   router (router.hip)   -> ids, weights, Q8_0 activation rows per token (K order of kperm)
 //   k_plan (router.hip)   -> pairs stably grouped by expert, each group cut into tiles of up to
-//                            16 MT pairs
+//                            32 pairs (batches of 8+ pairs per expert on average) or 4 (smaller)
+//   k_gateup_quad,        -> 4-pair tiles: one wave per (tile, 64 weight rows); the 16-block
+//   k_down_quad              v_mfma_i32_4x4x4_16b_i8 gives each lane its row's exact block sums
+//                            for the 4 pairs, so the f32 fold spends nothing on empty pair places
 //   k_gateup_mfma         -> per (tile, 4 row tiles of 32 gate + 32 up rows): int8 MFMA
 //                            (v_mfma_i32_16x16x32_i8, one 32-weight block per instruction) gives
 //                            each block's exact int32 sum for 16 pairs x 16 rows; the f32 terms
@@ -250,7 +253,8 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
     }
 }
 
-// Gate/up for one tile of up to 16 MT pairs of expert e: wave w takes row tile rt = 4 blockIdx.y + w
+// Gate/up for one tile (blockIdx.y) of up to 16 MT pairs of expert e: wave w takes row tile
+// rt = 4 blockIdx.x + w
 // (32 gate rows and the matching 32 up rows, one RVM_PACK_GATE_UP tile; pieces 0, 1 are gate rows
 // m and 16 + m, pieces 2, 3 the up rows). h = gelu(gate) * up is quantised per pair to one Q8_0
 // block of 32 (runtime/src/ops.rs:95-105) and stored in the K order of kperm.
@@ -265,14 +269,14 @@ __global__ __launch_bounds__(MW * 64) void k_gateup_mfma(const uint8_t *__restri
                                                          float *__restrict__ hsc, int d, int ff, int top_k) {
     constexpr int R = 16 * MT, KC = chunk_blocks<MT>();
     __shared__ TileLds<MT, 4, KC> sh;
-    const int tile = blockIdx.x;
+    const int tile = blockIdx.y;
     if (tile >= tiles[0]) return;
     const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
     const int cnt = min(R, gstart[e + 1] - k0);
     const int nb = d / QK, Tg = ff / 32;
     if (threadIdx.x < R) sh.row_of[threadIdx.x] = (int)threadIdx.x < cnt ? order[k0 + threadIdx.x] / top_k : -1;
     __syncthreads();
-    const int rt = blockIdx.y * MW + (threadIdx.x >> 6);
+    const int rt = blockIdx.x * MW + (threadIdx.x >> 6);
     const bool active = rt < Tg;
     float acc[MT][4][4];
     tile_sums<MT, 4, KC>(nib, scl, ((size_t)e * Tg + (active ? rt : 0)) * nb, nb, active, xq8, xsc, d, sh, acc);
@@ -301,7 +305,7 @@ __global__ __launch_bounds__(MW * 64) void k_gateup_mfma(const uint8_t *__restri
     }
 }
 
-// Down for one tile: wave w takes the 32-row down tile rt = 4 blockIdx.y + w (RVM_PACK_ROWS32:
+// Down for one tile (blockIdx.y): wave w takes the 32-row down tile rt = 4 blockIdx.x + w (RVM_PACK_ROWS32:
 // row r of the tile is plane lane r at block b < S, lane 32 + r at block S + b; pieces 0, 1 are
 // rows m and 16 + m).
 template <int MT>
@@ -313,14 +317,14 @@ __global__ __launch_bounds__(MW * 64) void k_down_mfma(const uint8_t *__restrict
                                                        float *__restrict__ y, int d, int ff) {
     constexpr int R = 16 * MT, KC = chunk_blocks<MT>();
     __shared__ TileLds<MT, 2, KC> sh;
-    const int tile = blockIdx.x;
+    const int tile = blockIdx.y;
     if (tile >= tiles[0]) return;
     const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
     const int cnt = min(R, gstart[e + 1] - k0);
     const int Sd = ff / 64, Td = d / 32;
     if (threadIdx.x < R) sh.row_of[threadIdx.x] = (int)threadIdx.x < cnt ? k0 + (int)threadIdx.x : -1;
     __syncthreads();
-    const int rt = blockIdx.y * MW + (threadIdx.x >> 6);
+    const int rt = blockIdx.x * MW + (threadIdx.x >> 6);
     const bool active = rt < Td;
     float acc[MT][2][4];
     tile_sums<MT, 2, KC>(nib, scl, ((size_t)e * Td + (active ? rt : 0)) * Sd, Sd, active, hq8, hsc, ff, sh, acc);
@@ -380,12 +384,238 @@ __global__ __launch_bounds__(256) void k_combine_pairs(const float *__restrict__
     *(float4 *)(out + (size_t)t * d + c) = o;
 }
 
-// Pairs per tile: enough m-tiles that a typical group fits one tile, so that its weights are
+// ---- Quad tiles: up to 4 pairs of one expert (small batches, where most groups hold a few
+// pairs and a 16-pair m-tile would spend most of its arithmetic on empty places) ----
+//
+// v_mfma_i32_4x4x4_16b_i8 computes 16 independent 4x4x4 products. In block q (lanes 4q .. 4q+3),
+// lane 4q + i gives row i of A and lane 4q + j column j of B (4 int8 each), and register i of
+// lane 4q + j receives D[i][j]. With row i of A = 4 activations of pair i (the same in every block)
+// and column j of block q = the 4 weights of row 4q + j, lane l accumulates the four pairs' sums
+// of weight row l: eight instructions cover one 32-weight block, and the f32 fold takes four
+// outputs per lane.
+constexpr int QUAD = MIN_TILE_PAIRS;  // pairs per quad tile
+
+// 16 times the int8 weights of one K slice of a weight dword (4-bit two's complement nibbles,
+// byte k holding elements 4g + k (low) and 16 + 4g + k (high)): the low nibbles moved to the top
+// of each byte, or the high nibbles in place. The products then sum to 16 sumi, exactly.
+__device__ __forceinline__ int slice_lo16(uint32_t p) { return (int)((p << 4) & 0xF0F0F0F0u); }
+__device__ __forceinline__ int slice_hi16(uint32_t p) { return (int)(p & 0xF0F0F0F0u); }
+
+// 16 times the block sums of this lane's weight row (entry w) with the four pairs' activations
+// (x0, x1: the 32 bytes of the block in the K order of kperm, dwords 2g and 2g + 1 holding the
+// elements of weight dword g's low and high nibbles).
+__device__ __forceinline__ v4i quad_sums16(uint4 w, uint4 x0, uint4 x1) {
+    v4i s = {0, 0, 0, 0};
+    s = __builtin_amdgcn_mfma_i32_4x4x4i8((int)x0.x, slice_lo16(w.x), s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_i32_4x4x4i8((int)x0.y, slice_hi16(w.x), s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_i32_4x4x4i8((int)x0.z, slice_lo16(w.y), s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_i32_4x4x4i8((int)x0.w, slice_hi16(w.y), s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_i32_4x4x4i8((int)x1.x, slice_lo16(w.z), s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_i32_4x4x4i8((int)x1.y, slice_hi16(w.z), s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_i32_4x4x4i8((int)x1.z, slice_lo16(w.w), s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_i32_4x4x4i8((int)x1.w, slice_hi16(w.w), s, 0, 0, 0);
+    return s;
+}
+
+// acc[i] = acc[i] + (sumi_i as f32) * (d_w * d_x_i). The scales are binary16 values, so d_w * d_x
+// is exact in f32 and so is its sixteenth: (16 sumi) * (d_w / 16 * d_x) rounds the same real
+// number as the reference's sumi * (d_w * d_x).
+__device__ __forceinline__ void quad_fold(float (&acc)[4], v4i s16, float dw16, float4 dx) {
+    acc[0] = acc[0] + (float)s16[0] * (dw16 * dx.x);
+    acc[1] = acc[1] + (float)s16[1] * (dw16 * dx.y);
+    acc[2] = acc[2] + (float)s16[2] * (dw16 * dx.z);
+    acc[3] = acc[3] + (float)s16[3] * (dw16 * dx.w);
+}
+
+// The wave's LDS region: the four pairs' activation rows (K order of kperm) at a pitch of
+// width + 16 bytes, so that the four rows start on different LDS banks, then their block scales,
+// [block][pair].
+__host__ __device__ constexpr int quad_pitch(int width) { return width + 16; }
+__host__ __device__ constexpr int quad_lds_bytes(int width) { return 4 * quad_pitch(width) + 4 * (width / QK) * 4; }
+
+// Copies the rows src_r = src + row_r * width (and scales ssrc + row_r * nb) of the wave's four
+// pairs into its LDS region; row_r comes from lane r of rowv.
+__device__ __forceinline__ void stage_quad_rows(const int8_t *__restrict__ src, const float *__restrict__ ssrc,
+                                                int rowv, int width, uint8_t *lds) {
+    const int lane = threadIdx.x & 63, nb = width / QK, pcs = width / 16, P = quad_pitch(width);
+    int row[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) row[r] = __shfl(rowv, r);
+    for (int p = lane; p < 4 * pcs; p += 64) {
+        const int r = p / pcs, c = p - r * pcs;
+        const int sr = r == 0 ? row[0] : (r == 1 ? row[1] : (r == 2 ? row[2] : row[3]));
+        *(uint4 *)(lds + r * P + c * 16) = *(const uint4 *)(src + (size_t)sr * width + c * 16);
+    }
+    float *sl = (float *)(lds + 4 * P);
+    for (int p = lane; p < 4 * nb; p += 64) {
+        const int r = p / nb, b = p - r * nb;
+        const int sr = r == 0 ? row[0] : (r == 1 ? row[1] : (r == 2 ? row[2] : row[3]));
+        sl[4 * b + r] = ssrc[(size_t)sr * nb + b];
+    }
+    wave_lds_sync();
+}
+
+// The four pairs' sequential folds of this lane's weight row over blocks 0 .. nb-1 (a multiple of
+// QD). entry(b): the lane's 16-byte weight entry of block b (its scale has the same index in scl);
+// stage(): fills lds, the wave's staged rows (the lane's pair is lane & 3). The weight loads run QD
+// blocks ahead in a ring of registers; past the last block they re-read it (unused).
+template <int QD, class Entry, class Stage>
+__device__ __forceinline__ void quad_row_sums(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl,
+                                              Entry entry, Stage stage, const uint8_t *lds, int width,
+                                              float (&acc)[4]) {
+    const int nb = width / QK, i = threadIdx.x & 3;
+    const uint8_t *xl = lds + i * quad_pitch(width);
+    const float4 *sl = (const float4 *)(lds + 4 * quad_pitch(width));
+    uint4 w[QD];
+    uint32_t s[QD];
+    auto load = [&](int u, int b) {
+        b = min(b, nb - 1);
+        const size_t e = entry(b);
+        w[u] = nib[e];
+        s[u] = scl[e];
+    };
+    // The first round only loads (and then stages the activation rows, their loads behind the
+    // weights'): it is the same code as the later rounds, so the loads are issued in the same order
+    // (one block's loads after each block's arithmetic) and each block waits for its own loads only.
+#pragma clang loop unroll(disable)
+    for (int b0 = -QD; b0 < nb; b0 += QD) {
+#pragma unroll
+        for (int u = 0; u < QD; ++u) {
+            if (b0 >= 0) {
+                const int b = b0 + u;
+                const uint4 x0 = *(const uint4 *)(xl + 32 * b), x1 = *(const uint4 *)(xl + 32 * b + 16);
+                quad_fold(acc, quad_sums16(w[u], x0, x1), h2f((uint16_t)s[u]) * 0.0625f, sl[b]);
+            }
+            load(u, b0 + u + QD);
+        }
+        if (b0 < 0) stage();
+    }
+}
+
+// Ring depth for nb blocks: a divisor of nb, so that the loop has no partial round.
+inline int quad_depth(int nb) { return nb % 11 == 0 ? 11 : (nb % 8 == 0 ? 8 : 2); }
+
+// Gate/up for one quad tile (up to 4 pairs of expert e) and one 64-row tile rt
+// (RVM_PACK_GATE_UP: lane l < 32 is gate row 32 rt + l, lane l >= 32 the matching up row), one
+// wave per workgroup. Lanes < 32 then form h of pairs 0 and 1, lanes >= 32 those of pairs 2 and 3 (gelu(gate) * up, runtime/src/exec.rs:626-630), each half-wave
+// quantising its pair's 32 values to one Q8_0 block (runtime/src/ops.rs:95-105) stored in the K
+// order of kperm.
+template <int QD>
+__global__ __launch_bounds__(64) void k_gateup_quad(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl,
+                                                     const int32_t *__restrict__ tiles,
+                                                     const int32_t *__restrict__ gstart,
+                                                     const int32_t *__restrict__ order,
+                                                     const int8_t *__restrict__ xq8, const float *__restrict__ xsc,
+                                                     int8_t *__restrict__ hq8, float *__restrict__ hsc, int d, int ff,
+                                                     int top_k) {
+    extern __shared__ uint4 quad_lds[];
+    const int tile = blockIdx.y;
+    if (tile >= tiles[0]) return;
+    const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
+    const int cnt = min(QUAD, gstart[e + 1] - k0);
+    const int lane = threadIdx.x, rt = blockIdx.x, nb = d / QK, Tg = ff / 32;
+    uint8_t *lds = (uint8_t *)quad_lds;
+    // the rows of the quad's pairs; a missing pair takes pair 0's row and is not stored
+    const int tok = lane < 4 ? order[k0 + (lane < cnt ? lane : 0)] / top_k : 0;
+    const size_t tb = ((size_t)e * Tg + rt) * nb;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    quad_row_sums<QD>(
+        nib, scl, [&](int b) { return (tb + (size_t)b) * 64 + lane; },
+        [&]() { stage_quad_rows(xq8, xsc, tok, d, lds); }, lds, d, acc);
+    float o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = __shfl_xor(acc[i], 32);
+    const bool lo = lane < 32;
+    const float hA = gelu(lo ? acc[0] : o[2]) * (lo ? o[0] : acc[2]);
+    const float hB = gelu(lo ? acc[1] : o[3]) * (lo ? o[1] : acc[3]);
+    uint16_t dA, dB;
+    const int qA = quant_q8_half(hA, &dA), qB = quant_q8_half(hB, &dB);
+    const int j = lane & 31, pA = lo ? 0 : 2;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int pr = pA + k;
+        if (pr < cnt) {
+            hq8[(size_t)(k0 + pr) * ff + rt * QK + kperm(j)] = (int8_t)(k ? qB : qA);
+            if (j == 0) hsc[(size_t)(k0 + pr) * Tg + rt] = h2f(k ? dB : dA);
+        }
+    }
+}
+
+// Down for one quad tile and 64 rows (two RVM_PACK_ROWS32 tiles: lane l is row 64 x + l, in tile
+// 2 x + l / 32 at place l & 31, block b at step b mod S, half b / S), one wave per workgroup.
+template <int QD>
+__global__ __launch_bounds__(64) void k_down_quad(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl,
+                                                   const int32_t *__restrict__ tiles,
+                                                   const int32_t *__restrict__ gstart, const int8_t *__restrict__ hq8,
+                                                   const float *__restrict__ hsc, float *__restrict__ y, int d,
+                                                   int ff) {
+    extern __shared__ uint4 quad_lds[];
+    const int tile = blockIdx.y;
+    if (tile >= tiles[0]) return;
+    const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
+    const int cnt = min(QUAD, gstart[e + 1] - k0);
+    const int lane = threadIdx.x, S = ff / 64, Td = d / 32;
+    uint8_t *lds = (uint8_t *)quad_lds;
+    const size_t tb = ((size_t)e * Td + 2 * blockIdx.x + (lane >> 5)) * S;
+    const int place = lane & 31;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    quad_row_sums<QD>(
+        nib, scl,
+        [&](int b) {
+            const int half = b >= S ? 1 : 0;
+            return (tb + (size_t)(b - half * S)) * 64 + 32 * half + place;
+        },
+        [&]() { stage_quad_rows(hq8, hsc, k0 + (lane < cnt ? lane : 0), ff, lds); }, lds, ff, acc);
+    const int row = 64 * blockIdx.x + lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (i < cnt) y[(size_t)(k0 + i) * d + row] = acc[i];
+}
+
+template <class F>
+int with_quad_depth(int nb, F &&f) {
+    switch (quad_depth(nb)) {
+        case 11: return f(std::integral_constant<int, 11>{});
+        case 8: return f(std::integral_constant<int, 8>{});
+        default: return f(std::integral_constant<int, 2>{});
+    }
+}
+
+int launch_experts_quad(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &lay) {
+    const int32_t *tiles = (const int32_t *)(w + lay.tiles);
+    const int32_t *gstart = (const int32_t *)(w + lay.gstart);
+    const int nt = (int)max_tiles(L, n_tok, QUAD);
+    const size_t gu_entries = (size_t)L->n_exp * 2 * L->ff * (L->d / QK);
+    const uint4 *gnib = (const uint4 *)L->gate_up;
+    const uint16_t *gscl = (const uint16_t *)((const uint8_t *)L->gate_up + gu_entries * 16);
+    int rc = with_quad_depth(L->d / QK, [&](auto qd) {
+        hipLaunchKernelGGL(k_gateup_quad<decltype(qd)::value>, dim3(L->ff / 32, nt), dim3(64), quad_lds_bytes(L->d),
+                           cur_stream(),
+                           gnib, gscl, tiles, gstart,
+                           (const int32_t *)(w + lay.order), (const int8_t *)(w + lay.xq8),
+                           (const float *)(w + lay.xsc), (int8_t *)(w + lay.hq8), (float *)(w + lay.hsc), L->d, L->ff,
+                           L->top_k);
+        return launched();
+    });
+    if (rc) return rc;
+    const size_t dn_entries = (size_t)L->n_exp * L->d * (L->ff / QK);
+    const uint4 *dnib = (const uint4 *)L->down;
+    const uint16_t *dscl = (const uint16_t *)((const uint8_t *)L->down + dn_entries * 16);
+    return with_quad_depth(L->ff / QK, [&](auto qd) {
+        hipLaunchKernelGGL(k_down_quad<decltype(qd)::value>, dim3(L->d / 64, nt), dim3(64), quad_lds_bytes(L->ff),
+                           cur_stream(), dnib, dscl, tiles, gstart,
+                           (const int8_t *)(w + lay.hq8), (const float *)(w + lay.hsc), (float *)(w + lay.y), L->d,
+                           L->ff);
+        return launched();
+    });
+}
+
+// Pairs per tile: quads while the groups are small (fewer pairs than 8 per expert on average),
+// else 32 (two 16-pair m-tiles), so that a typical group fits one tile and its weights are
 // streamed once.
-inline int tile_mt(const rvm_layer *L, int n_tok) {
+inline int tile_pairs(const rvm_layer *L, int n_tok) {
     const long pairs = (long)n_tok * L->top_k;
-    if (pairs >= 8L * L->n_exp) return 2;
-    return 1;
+    return pairs >= 8L * L->n_exp ? 32 : QUAD;
 }
 
 template <int MT>
@@ -396,7 +626,7 @@ int launch_experts(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &la
     const size_t gu_entries = (size_t)L->n_exp * 2 * L->ff * (L->d / QK);
     const uint8_t *gnib = (const uint8_t *)L->gate_up;
     const uint16_t *gscl = (const uint16_t *)(gnib + gu_entries * 16);
-    hipLaunchKernelGGL(k_gateup_mfma<MT>, dim3(nt, grid_blocks(L->ff / 32, MW)), dim3(MW * 64), 0, cur_stream(), gnib,
+    hipLaunchKernelGGL(k_gateup_mfma<MT>, dim3(grid_blocks(L->ff / 32, MW), nt), dim3(MW * 64), 0, cur_stream(), gnib,
                        gscl, tiles, gstart, (const int32_t *)(w + lay.order), (const int8_t *)(w + lay.xq8),
                        (const float *)(w + lay.xsc), (int8_t *)(w + lay.hq8), (float *)(w + lay.hsc), L->d, L->ff,
                        L->top_k);
@@ -405,7 +635,7 @@ int launch_experts(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &la
     const size_t dn_entries = (size_t)L->n_exp * L->d * (L->ff / QK);
     const uint8_t *dnib = (const uint8_t *)L->down;
     const uint16_t *dscl = (const uint16_t *)(dnib + dn_entries * 16);
-    hipLaunchKernelGGL(k_down_mfma<MT>, dim3(nt, grid_blocks(L->d / 32, MW)), dim3(MW * 64), 0, cur_stream(), dnib,
+    hipLaunchKernelGGL(k_down_mfma<MT>, dim3(grid_blocks(L->d / 32, MW), nt), dim3(MW * 64), 0, cur_stream(), dnib,
                        dscl, tiles, gstart, (const int8_t *)(w + lay.hq8), (const float *)(w + lay.hsc),
                        (float *)(w + lay.y), L->d, L->ff);
     return launched();
@@ -427,12 +657,11 @@ extern "C" int rvm_moe_forward(const rvm_layer *L, const float *x, float *out, i
     int32_t *pos_of = (int32_t *)(w + lay.pos_of);
     int rc = launch_router(L, x, n_tok, flags, eps, w, lay, ids, wts, nullptr, true);
     if (rc) return rc;
-    const int mt = tile_mt(L, n_tok);
+    const int cap = tile_pairs(L, n_tok);
     if ((rc = launch_plan(ids, n_tok * L->top_k, L->n_exp, (int32_t *)(w + lay.order), pos_of,
-                          (int32_t *)(w + lay.gstart), (int32_t *)(w + lay.tiles), 16 * mt)))
+                          (int32_t *)(w + lay.gstart), (int32_t *)(w + lay.tiles), cap)))
         return rc;
-    rc = mt == 4 ? launch_experts<4>(L, n_tok, w, lay)
-                 : (mt == 2 ? launch_experts<2>(L, n_tok, w, lay) : launch_experts<1>(L, n_tok, w, lay));
+    rc = cap == QUAD ? launch_experts_quad(L, n_tok, w, lay) : launch_experts<2>(L, n_tok, w, lay);
     if (rc) return rc;
     hipLaunchKernelGGL(k_combine_pairs, dim3(grid_blocks(L->d / 4, 256), n_tok), dim3(256), 0, cur_stream(),
                        (const float *)(w + lay.y), pos_of, ids, wts, L->down_scale, out, L->top_k, L->d);

@@ -33,7 +33,8 @@ constexpr int ACT_DW = 12;
 constexpr uint32_t ONES4 = 0x11111111u;
 constexpr int MAX_TOKENS = 65535;  // tokens per call (the router grid's y dimension)
 constexpr int MAX_TOP_K = 8;       // experts per token
-constexpr int MTILE = 16;          // pairs per MFMA m-tile; a batched tile holds 1, 2 or 4 of them
+constexpr int MTILE = 16;          // pairs per MFMA m-tile
+constexpr int MIN_TILE_PAIRS = 4;  // the smallest batched tile (quad tiles of small batches)
 
 // Library state (runtime.hip).
 hipStream_t cur_stream();
@@ -240,15 +241,17 @@ struct WsLayout {
     size_t xsc;     // f32[n_tok][d/32]: their scales
     size_t hq8;     // i8[pairs][ff]: plain Q8_0 values of h, in plan order (batched path)
     size_t hsc;     // f32[pairs][ff/32]
-    size_t tiles;   // i32[1 + 2 max_tiles]: the plan's 16-pair tiles
+    size_t tiles;   // i32[1 + 2 max_tiles]: the plan's tiles (4 or 32 pairs)
     size_t total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Upper bound on the plan's tiles of up to cap pairs: every group adds at most one partial tile.
+// Upper bound on the plan's tiles of up to cap pairs: a group of n pairs takes ceil(n / cap) <=
+// (n + cap - 1) / cap tiles, and there are at most min(n_exp, pairs) groups.
 inline size_t max_tiles(const rvm_layer *L, int n_tok, int cap) {
-    return ((size_t)n_tok * L->top_k + cap - 1) / cap + (size_t)L->n_exp;
+    const size_t pairs = (size_t)n_tok * L->top_k, groups = pairs < (size_t)L->n_exp ? pairs : (size_t)L->n_exp;
+    return (pairs + (size_t)(cap - 1) * groups) / cap;
 }
 
 inline WsLayout ws_layout(const rvm_layer *L, int n_tok) {
@@ -276,7 +279,7 @@ inline WsLayout ws_layout(const rvm_layer *L, int n_tok) {
     w.xsc = take((size_t)n_tok * (L->d / QK) * 4);
     w.hq8 = take(pairs * L->ff);
     w.hsc = take(pairs * (L->ff / QK) * 4);
-    w.tiles = take((1 + 2 * max_tiles(L, n_tok, MTILE)) * 4);
+    w.tiles = take((1 + 2 * max_tiles(L, n_tok, MIN_TILE_PAIRS)) * 4);
     w.total = o;
     return w;
 }

@@ -203,6 +203,24 @@ def test_forward_ragged_zipf_matches_oracle_and_decode(gpu, orc):
     del rng
 
 
+@pytest.mark.parametrize("n", [2, 5, 127, 128])
+def test_forward_batch_sizes_are_batch_invariant(gpu, n):
+    """Batches on both sides of the tile-size switch (4-pair tiles below 8 pairs per expert on
+    average: 127 tokens and fewer; 32-pair tiles from 128 tokens): groups of one pair up to full
+    tiles. Every checked token's row equals its single-token decode bit for bit."""
+    L = get_layer(0)[0]
+    x = synth.tokens(SEED + 7, n)
+    print(f"[batch] {n} tokens", flush=True)
+    ws = moe.Workspace(L, n)
+    xd, out = dev(x), DevBuf(n * D * 4)
+    moe.forward(L, xd, out, n, ws)
+    got = out.download(np.float32, n * D).reshape(n, D)
+    ws1, o1 = moe.Workspace(L, 1), DevBuf(D * 4)
+    for t in sorted({0, 1, n // 2, n - 1}):
+        moe.decode(L, xd, o1, ws1, x_off=t * D * 4)
+        assert np.array_equal(o1.download(np.float32, D), got[t]), t
+
+
 def test_prefill_512_is_batch_invariant(gpu, orc):
     key = get_layer(0)
     L = key[0]
