@@ -28,6 +28,12 @@ namespace rvm {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int MW = 4;  // waves (row tiles) per workgroup
+
+// Workgroups go to the 8 XCDs in turn, by linear index. A grid row of a multiple of 8 workgroups
+// sends row tile x of every tile to the same XCD, so the tiles of one expert share its L2 there
+// (the small-batch kernels, where a popular expert has several tiles; the arithmetic-bound batched
+// kernels keep every XCD busy instead).
+inline int xcd_rows(int n) { return (n + 7) & ~7; }
 // K blocks per chunk (a template parameter of the tile loop; 8 measured slower for one m-tile)
 template <int MT>
 constexpr int chunk_blocks() { return 4; }
@@ -458,7 +464,7 @@ __device__ __forceinline__ void stage_quad_rows(const int8_t *__restrict__ src, 
 // The four pairs' sequential folds of this lane's weight row over blocks 0 .. nb-1 (a multiple of
 // QD). entry(b): the lane's 16-byte weight entry of block b (its scale has the same index in scl);
 // stage(): fills lds, the wave's staged rows (the lane's pair is lane & 3). The weight loads run QD
-// blocks ahead in a ring of registers; past the last block they re-read it (unused).
+// blocks ahead in a ring of registers.
 template <int QD, class Entry, class Stage>
 __device__ __forceinline__ void quad_row_sums(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl,
                                               Entry entry, Stage stage, const uint8_t *lds, int width,
@@ -469,31 +475,35 @@ __device__ __forceinline__ void quad_row_sums(const uint4 *__restrict__ nib, con
     uint4 w[QD];
     uint32_t s[QD];
     auto load = [&](int u, int b) {
-        b = min(b, nb - 1);
         const size_t e = entry(b);
         w[u] = nib[e];
         s[u] = scl[e];
     };
+    auto compute = [&](int u, int b) {
+        const uint4 x0 = *(const uint4 *)(xl + 32 * b), x1 = *(const uint4 *)(xl + 32 * b + 16);
+        quad_fold(acc, quad_sums16(w[u], x0, x1), h2f((uint16_t)s[u]) * 0.0625f, sl[b]);
+    };
     // The first round only loads (and then stages the activation rows, their loads behind the
     // weights'): it is the same code as the later rounds, so the loads are issued in the same order
     // (one block's loads after each block's arithmetic) and each block waits for its own loads only.
+    // The last round, blocks nb - QD .. nb - 1, loads nothing.
 #pragma clang loop unroll(disable)
-    for (int b0 = -QD; b0 < nb; b0 += QD) {
+    for (int b0 = -QD; b0 < nb - QD; b0 += QD) {
 #pragma unroll
         for (int u = 0; u < QD; ++u) {
-            if (b0 >= 0) {
-                const int b = b0 + u;
-                const uint4 x0 = *(const uint4 *)(xl + 32 * b), x1 = *(const uint4 *)(xl + 32 * b + 16);
-                quad_fold(acc, quad_sums16(w[u], x0, x1), h2f((uint16_t)s[u]) * 0.0625f, sl[b]);
-            }
+            if (b0 >= 0) compute(u, b0 + u);
             load(u, b0 + u + QD);
         }
         if (b0 < 0) stage();
     }
+#pragma unroll
+    for (int u = 0; u < QD; ++u) compute(u, nb - QD + u);
 }
 
-// Ring depth for nb blocks: a divisor of nb, so that the loop has no partial round.
-inline int quad_depth(int nb) { return nb % 11 == 0 ? 11 : (nb % 8 == 0 ? 8 : 2); }
+// Ring depth for nb blocks, a divisor of nb (nb is even), so that the loop has no partial round:
+// 8 for the long gate/up rows; 2 for short rows (the down rows, 22 blocks at ff = 704, measured
+// faster at 2 than at 11).
+inline int quad_depth(int nb) { return nb >= 64 && nb % 8 == 0 ? 8 : 2; }
 
 // Gate/up for one quad tile (up to 4 pairs of expert e) and one 64-row tile rt
 // (RVM_PACK_GATE_UP: lane l < 32 is gate row 32 rt + l, lane l >= 32 the matching up row), one
@@ -514,6 +524,7 @@ __global__ __launch_bounds__(64) void k_gateup_quad(const uint4 *__restrict__ ni
     const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
     const int cnt = min(QUAD, gstart[e + 1] - k0);
     const int lane = threadIdx.x, rt = blockIdx.x, nb = d / QK, Tg = ff / 32;
+    if (rt >= Tg) return;  // the padding of the grid's rows
     uint8_t *lds = (uint8_t *)quad_lds;
     // the rows of the quad's pairs; a missing pair takes pair 0's row and is not stored
     const int tok = lane < 4 ? order[k0 + (lane < cnt ? lane : 0)] / top_k : 0;
@@ -555,6 +566,7 @@ __global__ __launch_bounds__(64) void k_down_quad(const uint4 *__restrict__ nib,
     const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
     const int cnt = min(QUAD, gstart[e + 1] - k0);
     const int lane = threadIdx.x, S = ff / 64, Td = d / 32;
+    if ((int)blockIdx.x >= d / 64) return;  // the padding of the grid's rows
     uint8_t *lds = (uint8_t *)quad_lds;
     const size_t tb = ((size_t)e * Td + 2 * blockIdx.x + (lane >> 5)) * S;
     const int place = lane & 31;
@@ -574,11 +586,8 @@ __global__ __launch_bounds__(64) void k_down_quad(const uint4 *__restrict__ nib,
 
 template <class F>
 int with_quad_depth(int nb, F &&f) {
-    switch (quad_depth(nb)) {
-        case 11: return f(std::integral_constant<int, 11>{});
-        case 8: return f(std::integral_constant<int, 8>{});
-        default: return f(std::integral_constant<int, 2>{});
-    }
+    if (quad_depth(nb) == 8) return f(std::integral_constant<int, 8>{});
+    return f(std::integral_constant<int, 2>{});
 }
 
 int launch_experts_quad(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &lay) {
@@ -589,7 +598,7 @@ int launch_experts_quad(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayou
     const uint4 *gnib = (const uint4 *)L->gate_up;
     const uint16_t *gscl = (const uint16_t *)((const uint8_t *)L->gate_up + gu_entries * 16);
     int rc = with_quad_depth(L->d / QK, [&](auto qd) {
-        hipLaunchKernelGGL(k_gateup_quad<decltype(qd)::value>, dim3(L->ff / 32, nt), dim3(64), quad_lds_bytes(L->d),
+        hipLaunchKernelGGL(k_gateup_quad<decltype(qd)::value>, dim3(xcd_rows(L->ff / 32), nt), dim3(64), quad_lds_bytes(L->d),
                            cur_stream(),
                            gnib, gscl, tiles, gstart,
                            (const int32_t *)(w + lay.order), (const int8_t *)(w + lay.xq8),
@@ -602,7 +611,7 @@ int launch_experts_quad(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayou
     const uint4 *dnib = (const uint4 *)L->down;
     const uint16_t *dscl = (const uint16_t *)((const uint8_t *)L->down + dn_entries * 16);
     return with_quad_depth(L->ff / QK, [&](auto qd) {
-        hipLaunchKernelGGL(k_down_quad<decltype(qd)::value>, dim3(L->d / 64, nt), dim3(64), quad_lds_bytes(L->ff),
+        hipLaunchKernelGGL(k_down_quad<decltype(qd)::value>, dim3(xcd_rows(L->d / 64), nt), dim3(64), quad_lds_bytes(L->ff),
                            cur_stream(), dnib, dscl, tiles, gstart,
                            (const int8_t *)(w + lay.hq8), (const float *)(w + lay.hsc), (float *)(w + lay.y), L->d,
                            L->ff);
