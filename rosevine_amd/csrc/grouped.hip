@@ -38,16 +38,18 @@ inline int xcd_rows(int n) { return (n + 7) & ~7; }
 template <int MT>
 constexpr int chunk_blocks() { return 4; }
 
-// 8 int8 weights from one dword of a packed Q4_0 entry (bytes 4g .. 4g+3, each nibble the 4-bit
-// two's complement weight): the low nibbles (elements 4g .. 4g+3) then the high nibbles
-// (16+4g .. 16+4g+3), the K group order of kperm. Per byte, ((p ^ 8) + 0x78) ^ 0x80 is p
-// sign-extended, with no carry between bytes.
-__device__ __forceinline__ uint32_t nib8(uint32_t p) {
-    const uint32_t t = (p & 0x0F0F0F0Fu) ^ 0x08080808u;
-    return (t + 0x78787878u) ^ 0x80808080u;
-}
-__device__ __forceinline__ long weights8(uint32_t p) {
-    return (long)(((uint64_t)nib8(p >> 4) << 32) | nib8(p));
+// 16 times the int8 weights of one K slice of a packed Q4_0 entry's dword g (bytes 4g .. 4g+3,
+// each nibble the 4-bit two's complement weight; byte k holds elements 4g + k in its low nibble and
+// 16 + 4g + k in its high one): the low nibbles moved to the top of each byte, or the high nibbles
+// in place. Products with these sum to 16 sumi, exactly (|16 sumi| < 2^20); the activation scales
+// are staged divided by 16, which is exact for binary16 values, so the folds see the reference's
+// terms: (16 sumi) * (d_w * d_x / 16) rounds the same real number as sumi * (d_w * d_x).
+__device__ __forceinline__ int slice_lo16(uint32_t p) { return (int)((p << 4) & 0xF0F0F0F0u); }
+__device__ __forceinline__ int slice_hi16(uint32_t p) { return (int)(p & 0xF0F0F0F0u); }
+// The 8 weights of dword p for a 16x16x32 MFMA K group: elements 4g .. 4g+3, then 16+4g .. 16+4g+3
+// (the K group order of kperm), each times 16.
+__device__ __forceinline__ long weights16(uint32_t p) {
+    return (long)(((uint64_t)(uint32_t)slice_hi16(p) << 32) | (uint32_t)slice_lo16(p));
 }
 
 // Max over each row of 16 lanes (the lanes of one MFMA K group) of non-NaN values.
@@ -58,7 +60,8 @@ __device__ __forceinline__ float row16_max(float m) {
     return maxf_bits(m, dpp<0x140>(__builtin_bit_cast(uint32_t, m)));
 }
 
-// The f32 fold of one block into acc: acc[i] = acc[i] + (sumi as f32) * (d_w * d_x[i]).
+// The f32 fold of one block into acc: acc[i] = acc[i] + (16 sumi as f32) * (d_w * d_x[i] / 16),
+// the reference's term sumi * (d_w * d_x[i]) (dx holds d_x / 16).
 __device__ __forceinline__ void fold_block(float (&acc)[4], v4i sumi, float dw, float4 dx) {
     acc[0] = acc[0] + (float)sumi[0] * (dw * dx.x);
     acc[1] = acc[1] + (float)sumi[1] * (dw * dx.y);
@@ -174,7 +177,7 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
 #pragma unroll
         for (int k = 0; k < SI; ++k) {
             const bool ok = sok[k] && c * KC + skbx[k] < nb;
-            if (skbx[k] >= 0) sh.ss[buf][threadIdx.x + k * NT] = ok ? sr[k] : 0.0f;
+            if (skbx[k] >= 0) sh.ss[buf][threadIdx.x + k * NT] = ok ? sr[k] * 0.0625f : 0.0f;  // d_x / 16
         }
     };
     auto compute = [&](int c, int buf, const uint32_t (&wn)[KC][NR], const uint32_t (&wsc)[SPL / 2]) {
@@ -215,7 +218,7 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
             v4i sm[MT][NR];
 #pragma unroll
             for (int r = 0; r < NR; ++r) {
-                const long bw = weights8(wn[kb][r]);
+                const long bw = weights16(wn[kb][r]);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
                     sm[mt][r] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[mt], bw, v4i{0, 0, 0, 0}, 0, 0, 0);
@@ -401,12 +404,6 @@ __global__ __launch_bounds__(256) void k_combine_pairs(const float *__restrict__
 // outputs per lane.
 constexpr int QUAD = MIN_TILE_PAIRS;  // pairs per quad tile
 
-// 16 times the int8 weights of one K slice of a weight dword (4-bit two's complement nibbles,
-// byte k holding elements 4g + k (low) and 16 + 4g + k (high)): the low nibbles moved to the top
-// of each byte, or the high nibbles in place. The products then sum to 16 sumi, exactly.
-__device__ __forceinline__ int slice_lo16(uint32_t p) { return (int)((p << 4) & 0xF0F0F0F0u); }
-__device__ __forceinline__ int slice_hi16(uint32_t p) { return (int)(p & 0xF0F0F0F0u); }
-
 // 16 times the block sums of this lane's weight row (entry w) with the four pairs' activations
 // (x0, x1: the 32 bytes of the block in the K order of kperm, dwords 2g and 2g + 1 holding the
 // elements of weight dword g's low and high nibbles).
@@ -423,19 +420,18 @@ __device__ __forceinline__ v4i quad_sums16(uint4 w, uint4 x0, uint4 x1) {
     return s;
 }
 
-// acc[i] = acc[i] + (sumi_i as f32) * (d_w * d_x_i). The scales are binary16 values, so d_w * d_x
-// is exact in f32 and so is its sixteenth: (16 sumi) * (d_w / 16 * d_x) rounds the same real
-// number as the reference's sumi * (d_w * d_x).
-__device__ __forceinline__ void quad_fold(float (&acc)[4], v4i s16, float dw16, float4 dx) {
-    acc[0] = acc[0] + (float)s16[0] * (dw16 * dx.x);
-    acc[1] = acc[1] + (float)s16[1] * (dw16 * dx.y);
-    acc[2] = acc[2] + (float)s16[2] * (dw16 * dx.z);
-    acc[3] = acc[3] + (float)s16[3] * (dw16 * dx.w);
+// acc[i] = acc[i] + (16 sumi_i as f32) * (d_w * d_x_i / 16), the reference's term (dx holds the
+// four pairs' d_x / 16).
+__device__ __forceinline__ void quad_fold(float (&acc)[4], v4i s16, float dw, float4 dx) {
+    acc[0] = acc[0] + (float)s16[0] * (dw * dx.x);
+    acc[1] = acc[1] + (float)s16[1] * (dw * dx.y);
+    acc[2] = acc[2] + (float)s16[2] * (dw * dx.z);
+    acc[3] = acc[3] + (float)s16[3] * (dw * dx.w);
 }
 
 // The wave's LDS region: the four pairs' activation rows (K order of kperm) at a pitch of
-// width + 16 bytes, so that the four rows start on different LDS banks, then their block scales,
-// [block][pair].
+// width + 16 bytes, so that the four rows start on different LDS banks, then their block scales
+// divided by 16, [block][pair].
 __host__ __device__ constexpr int quad_pitch(int width) { return width + 16; }
 __host__ __device__ constexpr int quad_lds_bytes(int width) { return 4 * quad_pitch(width) + 4 * (width / QK) * 4; }
 
@@ -456,7 +452,7 @@ __device__ __forceinline__ void stage_quad_rows(const int8_t *__restrict__ src, 
     for (int p = lane; p < 4 * nb; p += 64) {
         const int r = p / nb, b = p - r * nb;
         const int sr = r == 0 ? row[0] : (r == 1 ? row[1] : (r == 2 ? row[2] : row[3]));
-        sl[4 * b + r] = ssrc[(size_t)sr * nb + b];
+        sl[4 * b + r] = ssrc[(size_t)sr * nb + b] * 0.0625f;  // d_x / 16
     }
     wave_lds_sync();
 }
@@ -481,7 +477,7 @@ __device__ __forceinline__ void quad_row_sums(const uint4 *__restrict__ nib, con
     };
     auto compute = [&](int u, int b) {
         const uint4 x0 = *(const uint4 *)(xl + 32 * b), x1 = *(const uint4 *)(xl + 32 * b + 16);
-        quad_fold(acc, quad_sums16(w[u], x0, x1), h2f((uint16_t)s[u]) * 0.0625f, sl[b]);
+        quad_fold(acc, quad_sums16(w[u], x0, x1), h2f((uint16_t)s[u]), sl[b]);
     };
     // The first round only loads (and then stages the activation rows, their loads behind the
     // weights'): it is the same code as the later rounds, so the loads are issued in the same order
