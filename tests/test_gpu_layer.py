@@ -203,12 +203,13 @@ def test_forward_ragged_zipf_matches_oracle_and_decode(gpu, orc):
     del rng
 
 
-@pytest.mark.parametrize("n", [2, 5, 127, 128])
-def test_forward_batch_sizes_are_batch_invariant(gpu, n):
+@pytest.mark.parametrize("n,extras", [(2, False), (5, False), (5, True), (127, False), (127, True), (128, False)])
+def test_forward_batch_sizes_are_batch_invariant(gpu, n, extras):
     """Batches on both sides of the tile-size switch (4-pair tiles below 8 pairs per expert on
     average: 127 tokens and fewer; 32-pair tiles from 128 tokens): groups of one pair up to full
-    tiles. Every checked token's row equals its single-token decode bit for bit."""
-    L = get_layer(0)[0]
+    tiles, with and without router bias and down scales. Every checked token's row equals its
+    single-token decode bit for bit."""
+    L = get_layer(0, bias=extras, ds=extras)[0]
     x = synth.tokens(SEED + 7, n)
     print(f"[batch] {n} tokens", flush=True)
     ws = moe.Workspace(L, n)
