@@ -16,8 +16,8 @@
  * known answers, independent implementations (numpy's IEEE half conversion, float32 sequential
  * accumulate, stable sort), closed forms, f64 brute force or exhaustive sweeps;
  * tests/test_oracle_mutations.py plants plausible mistakes in a copy of this file and shows that
- * those checks catch each one; tests/golden/ freezes small input/output vectors. Limits:
- * orc_dot_q8_avx2_order is held only to the exact-integer error bound (its lane order is the
+ * those checks catch each one; tests/golden/ freezes small input/output vectors. Parity
+ * unpinned: orc_dot_q8_avx2_order is held only to the exact-integer error bound (its lane order is the
  * CPU baseline's, not a value the GPU path is compared with), and the f32 operation order of
  * orc_gelu and of the combine follows the cited lines by reading, with the reference's own
  * bitwise combine test (runtime/tests/hip_ops.rs:421-439) as the check of the latter.
