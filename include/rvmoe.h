@@ -142,6 +142,11 @@ typedef struct rvm_layer {
 #define RVM_PRE_NORM 1     /* the layer input is rms_norm(x, eps) (runtime/src/ops.rs:131-139) */
 #define RVM_EXACT_SELECT 2 /* always recompute the router logits in the reference's order */
 
+/* From this many tokens a call folds every router logit in the reference's order (exact logits,
+ * ids and weights; no certificate and no fallbacks); decode and smaller batches rank by the
+ * certified f64 estimates, with the exact fallback. */
+#define RVM_FOLD_MIN_TOKENS 256
+
 /* Workspace bytes for n_tok tokens through rvm_moe_decode (n_tok = 1) or rvm_moe_forward.
  * A workspace is zeroed once with rvm_workspace_init and may be reused by later calls on the
  * same stream; concurrent calls need separate workspaces. */

@@ -179,6 +179,152 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void k_select(const double2 *__rest
     select_publish<F4, SEL_WAVES>(sh, top_k, ids + (size_t)tok * top_k, wts + (size_t)tok * top_k);
 }
 
+// ---- Large batches: the reference's logits, folded exactly ----
+// From FOLD_MIN_TOKENS tokens a batch holds enough (token, expert) pairs to fill the GPU with one
+// sequential fold per lane, which is cheaper than the f64 statistics and the certificate: lane l
+// of a wave is token t0 + l, the wave's expert is uniform, and each lane adds the f32 products
+// W_r[e][i] * x'[i] in element order from -0.0 (runtime/src/ops.rs:321-326), then the bias, so the
+// logits are the reference's bit for bit. The tile's 64 tokens are staged in LDS FKC columns at a
+// time (double-buffered, the next chunk's loads in flight), with the workgroup's router rows beside
+// them, read as LDS broadcasts (every wait in the loop is then on in-order LDS traffic; scalar loads
+// share the LDS wait counter and complete out of order, and taking the row from lanes with
+// v_readlane measured slower). Column quad q of token t sits at [q][t ^ (q & 7)], so the coalesced
+// stores (eight quads of one token) and the per-token reads (one quad of 64 tokens) are free of
+// bank conflicts. Workgroup g also
+// quantises the Q8_0 blocks of tokens g, g + gridDim.x, ... of each staged chunk
+// (runtime/src/ops.rs:95-105).
+constexpr int FOLD_MIN_TOKENS = RVM_FOLD_MIN_TOKENS;
+constexpr int FW = 4;     // waves (experts) per workgroup
+constexpr int FKC = 128;  // columns per staged chunk
+
+// rms_norm scale of every token (runtime/src/ops.rs:131-139), one wave per token, for the fold.
+template <int F4>
+__global__ __launch_bounds__(256) void k_norm_scales(const float *__restrict__ x, int n_tok, float eps,
+                                                     float *__restrict__ scale) {
+    const int t = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= n_tok) return;
+    float4 xv[F4];
+    const float s = load_x_chunk<F4>(x + (size_t)t * 256 * F4, lane, 1, eps, xv);
+    if (lane == 0) scale[t] = s;
+}
+
+template <int F4>
+__global__ __launch_bounds__(FW * 64) void k_router_fold(const float *__restrict__ W, const float *__restrict__ x,
+                                                         const float *__restrict__ bias,
+                                                         const float *__restrict__ scale, int n_tok, int n_exp,
+                                                         float *__restrict__ R, int8_t *__restrict__ xq8,
+                                                         float *__restrict__ xsc) {
+    constexpr int d = 256 * F4, nb = d / QK, NCH = d / FKC, KQ = FKC / 4, LD = 64 * KQ / (FW * 64);
+    static_assert(d % FKC == 0 && FKC % QK == 0 && KQ % 4 == 0, "whole blocks per chunk");
+    static_assert(FW * KQ <= FW * 64, "one row quad per thread");
+    __shared__ float4 xs[2][KQ][64];  // the tile's layer input, column quad q of token t at [q][t ^ (q & 7)]
+    __shared__ float4 wsh[2][FW][KQ];  // the workgroup's router rows
+    __shared__ float sc[64];
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int t0 = blockIdx.y * 64;
+    const int ew = blockIdx.x * FW + w;
+    if (tid < 64) sc[tid] = scale ? scale[min(t0 + tid, n_tok - 1)] : 1.0f;
+    // staging: thread tid moves quad (tid % KQ) of tokens tid / KQ + j (256 / KQ), j < LD, and
+    // threads below FW KQ quad (tid % KQ) of row tid / KQ
+    const int sq = tid % KQ, st = tid / KQ;
+    const bool wst = tid < FW * KQ;
+    const float *xrow[LD];
+#pragma unroll
+    for (int j = 0; j < LD; ++j) xrow[j] = x + (size_t)min(t0 + st + j * (256 / KQ), n_tok - 1) * d + 4 * sq;
+    const float *wrow = W + (size_t)min(blockIdx.x * FW + (wst ? st : 0), n_exp - 1) * d + 4 * sq;
+    float4 pf[LD], pw;
+#pragma unroll
+    for (int j = 0; j < LD; ++j) pf[j] = *(const float4 *)xrow[j];
+    pw = *(const float4 *)wrow;
+    __syncthreads();  // sc
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < LD; ++j) {
+            const int tt = st + j * (256 / KQ);
+            const float s = sc[tt];
+            const float4 v = scale ? make_float4(pf[j].x * s, pf[j].y * s, pf[j].z * s, pf[j].w * s) : pf[j];
+            xs[buf][sq][tt ^ (sq & 7)] = v;
+        }
+        if (wst) wsh[buf][st][sq] = pw;
+    };
+    stage(0);
+    __syncthreads();
+    // quantisation duty: tokens g, g + G, ... of the tile, 4 blocks each, one block per half-wave
+    const int G = gridDim.x, g = blockIdx.x;
+    const int njobs = (g < 64 ? (64 - g + G - 1) / G : 0) * (FKC / QK);
+    float acc = -0.0f;
+    for (int c = 0; c < NCH; ++c) {
+        const int buf = c & 1;
+        // unconditional loads (the last chunk loads itself again, unused), so that the wait counts
+        // stay exact: a conditional load makes the compiler wait for the whole prefetch
+        const int cn = min(c + 1, NCH - 1);
+#pragma unroll
+        for (int j = 0; j < LD; ++j) pf[j] = *(const float4 *)(xrow[j] + cn * FKC);
+        pw = *(const float4 *)(wrow + cn * FKC);
+        // 4 quads at a time (the row quad is the same address in every lane: a broadcast)
+#pragma unroll 2
+        for (int q0 = 0; q0 < KQ; q0 += 4) {
+            float4 wv[4], xv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                wv[q] = wsh[buf][w][q0 + q];
+                xv[q] = xs[buf][q0 + q][lane ^ ((q0 + q) & 7)];
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc = acc + wv[q].x * xv[q].x;
+                acc = acc + wv[q].y * xv[q].y;
+                acc = acc + wv[q].z * xv[q].z;
+                acc = acc + wv[q].w * xv[q].w;
+            }
+        }
+        for (int jp = 2 * w; jp < njobs; jp += 2 * FW) {
+            const int job = jp + (lane >> 5), j = lane & 31;
+            const bool ok = job < njobs;
+            const int tt = g + (ok ? job / (FKC / QK) : 0) * G, blk = job % (FKC / QK);
+            const int q = blk * (QK / 4) + (j >> 2);
+            const float4 v4 = xs[buf][q][tt ^ (q & 7)];
+            const float v = (j & 3) == 0 ? v4.x : (j & 3) == 1 ? v4.y : (j & 3) == 2 ? v4.z : v4.w;
+            uint16_t dbits;
+            const int qv = quant_q8_half(v, &dbits);
+            const int t = t0 + tt, hb = c * (FKC / QK) + blk;
+            if (ok && t < n_tok) {
+                xq8[(size_t)t * d + hb * QK + kperm(j)] = (int8_t)qv;
+                if (j == 0) xsc[(size_t)t * nb + hb] = h2f(dbits);
+            }
+        }
+        if (c + 1 < NCH) stage(buf ^ 1);
+        __syncthreads();
+    }
+    const int t = t0 + lane;
+    if (ew < n_exp && t < n_tok) R[(size_t)t * n_exp + ew] = bias ? acc + bias[ew] : acc;
+}
+
+// The reference's softmax and top-k from the exact logits, one wave per token.
+__global__ __launch_bounds__(256) void k_select_exact(const float *__restrict__ R, int n_tok, int n_exp, int top_k,
+                                                      int32_t *__restrict__ ids, float *__restrict__ wts,
+                                                      float *__restrict__ logits) {
+    __shared__ float sp[4][256];
+    __shared__ int sel[4][8];
+    __shared__ float wsel[4][8];
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + w;
+    if (t >= n_tok) return;  // the whole wave
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = lane + 64 * i < n_exp ? R[(size_t)t * n_exp + lane + 64 * i] : -INFINITY;
+    exact_softmax_top_k(r, n_exp, top_k, sp[w], sel[w], wsel[w], logits ? logits + (size_t)t * n_exp : nullptr,
+                        lane);
+    wave_lds_sync();
+    if (lane < top_k) {
+        ids[(size_t)t * top_k + lane] = sel[w][lane];
+        wts[(size_t)t * top_k + lane] = wsel[w][lane];
+    }
+}
+
 // Stable counting sort of pair ids by expert in one workgroup of 16 waves: wave w owns a
 // contiguous chunk of pairs; per-(wave, expert) counts are scanned in (expert, wave) order, then
 // each wave places its pairs 64 at a time, ranking equal experts among lower lanes with ballots.
@@ -286,6 +432,20 @@ int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, floa
             const int groups = grid_blocks(L->n_exp, RWAVES), qgroups = grid_blocks(L->d / QK, 2 * RWAVES);
             hipLaunchKernelGGL(k_router<F4>, dim3(groups + qgroups), dim3(RWAVES * 64), 0, cur_stream(), L->router, x,
                                L->n_exp, pre, eps, (double2 *)(ws + lay.stats), (uint32_t *)(ws + lay.xact));
+        } else if (select && n_tok >= FOLD_MIN_TOKENS) {  // large batches: exact logits, no certificate
+            float *R = (float *)(ws + lay.stats), *sc = R + (size_t)n_tok * L->n_exp;
+            if (pre) {
+                hipLaunchKernelGGL(k_norm_scales<F4>, dim3(grid_blocks(n_tok, 4)), dim3(256), 0, cur_stream(), x,
+                                   n_tok, eps, sc);
+                if (int rc = launched()) return rc;
+            }
+            hipLaunchKernelGGL(k_router_fold<F4>, dim3(grid_blocks(L->n_exp, FW), grid_blocks(n_tok, 64)),
+                               dim3(FW * 64), 0, cur_stream(), L->router, x, L->router_bias, pre ? sc : nullptr,
+                               n_tok, L->n_exp, R, (int8_t *)(ws + lay.xq8), (float *)(ws + lay.xsc));
+            if (int rc = launched()) return rc;
+            hipLaunchKernelGGL(k_select_exact, dim3(grid_blocks(n_tok, 4)), dim3(256), 0, cur_stream(), R, n_tok,
+                               L->n_exp, L->top_k, ids, wts, logits);
+            return launched();
         } else {  // batches: about 16 token groups, so that the rows are read that many times
             const int rt = max(1, n_tok / 16);
             hipLaunchKernelGGL(k_router_batch<F4>, dim3(grid_blocks(L->n_exp, BW), grid_blocks(n_tok, rt)),

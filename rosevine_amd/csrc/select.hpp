@@ -149,6 +149,55 @@ __device__ __forceinline__ void wave_top_k(const uint32_t (&k)[4], bool (&alive)
     }
 }
 
+// The reference's selection from its exact logits, one wave (runtime/src/exec.rs:507-517):
+// softmax (runtime/src/ops.rs:170-179: max ignoring NaN, numerators expf(R - max) correctly
+// rounded, their f64 sum in index order, inv = (1/sum) as f32, p * inv), top_k by total_cmp with
+// ties to the lower index (ops.rs:182-187), and the weights p_j / max(sum of the selected p in top
+// order, 2^-14). R[i] is expert lane + 64 i (-inf past n_exp); sp (256 floats), sel and wsel are
+// LDS of this wave; lg_t, when set, receives the logits. Every lane of the wave calls this.
+__device__ __forceinline__ void exact_softmax_top_k(const float (&R)[4], int n_exp, int top_k, float *sp, int *sel,
+                                                    float *wsel, float *lg_t, int lane) {
+    float Mf = -INFINITY;  // max ignoring NaN (runtime/src/ops.rs:171)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Mf = fmaxf(Mf, R[i]);
+    Mf = wave_max_f(Mf);
+    if (lg_t)
+        for (int i = 0; i < 4; ++i)
+            if (lane + 64 * i < n_exp) lg_t[lane + 64 * i] = R[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (lane + 64 * i < n_exp) sp[lane + 64 * i] = (float)exp((double)(R[i] - Mf));
+    wave_lds_sync();
+    float inv = 0.0f;
+    if (lane == 0) {
+        double sum = 0.0;
+        for (int j = 0; j < n_exp; ++j) sum += (double)sp[j];
+        inv = (float)(1.0 / sum);
+    }
+    inv = __shfl(inv, 0);
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = lane + 64 * i < n_exp ? sp[lane + 64 * i] * inv : 0.0f;
+    wave_lds_sync();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (lane + 64 * i < n_exp) sp[lane + 64 * i] = p[i];
+    uint32_t k[4];
+    bool alive[4];
+    int rk[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        alive[i] = lane + 64 * i < n_exp;
+        k[i] = alive[i] ? order_key(p[i]) : 0u;
+    }
+    wave_top_k(k, alive, top_k, rk, sel);
+    wave_lds_sync();
+    float s = -0.0f;
+    for (int j = 0; j < top_k; ++j) s = s + sp[sel[j]];
+    s = fmaxf(s, 1.0f / 16384.0f);
+    if (lane < top_k) wsel[lane] = sp[sel[lane]] / s;
+}
+
 // rms_norm of this lane's chunk xv of the layer input xt, in place (runtime/src/ops.rs:131-139:
 // f64 sum of squares, mean as f32, 1/sqrt(mean + eps)); every wave computes the same scale.
 template <int F4>
@@ -611,45 +660,7 @@ __device__ void select_token(SelShared<F4, NW> &sh, const double2 *__restrict__ 
             float R[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) R[i] = lane + 64 * i < n_exp ? sh.sR[lane + 64 * i] : -INFINITY;
-            float Mf = -INFINITY;  // max ignoring NaN (runtime/src/ops.rs:171)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) Mf = fmaxf(Mf, R[i]);
-            Mf = wave_max_f(Mf);
-            if (publish && lg_t)
-                for (int i = 0; i < 4; ++i)
-                    if (lane + 64 * i < n_exp) lg_t[lane + 64 * i] = R[i];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (lane + 64 * i < n_exp) sh.sp[lane + 64 * i] = (float)exp((double)(R[i] - Mf));
-            wave_lds_sync();
-            float inv = 0.0f;
-            if (lane == 0) {
-                double sum = 0.0;
-                for (int j = 0; j < n_exp; ++j) sum += (double)sh.sp[j];
-                inv = (float)(1.0 / sum);
-            }
-            inv = __shfl(inv, 0);
-            float p[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) p[i] = lane + 64 * i < n_exp ? sh.sp[lane + 64 * i] * inv : 0.0f;
-            wave_lds_sync();
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (lane + 64 * i < n_exp) sh.sp[lane + 64 * i] = p[i];
-            uint32_t k[4];
-            bool alive[4];
-            int rk[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                alive[i] = lane + 64 * i < n_exp;
-                k[i] = alive[i] ? order_key(p[i]) : 0u;
-            }
-            wave_top_k(k, alive, top_k, rk, sh.sel);
-            wave_lds_sync();
-            float s = -0.0f;
-            for (int j = 0; j < top_k; ++j) s = s + sh.sp[sh.sel[j]];
-            s = fmaxf(s, 1.0f / 16384.0f);
-            if (lane < top_k) sh.wsel[lane] = sh.sp[sh.sel[lane]] / s;
+            exact_softmax_top_k(R, n_exp, top_k, sh.sp, sh.sel, sh.wsel, publish ? lg_t : nullptr, lane);
         }
     }
     __syncthreads();

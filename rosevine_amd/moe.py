@@ -17,6 +17,11 @@ from . import hip
 from .hip import DevBuf, RvmLayer, check, lib
 
 
+# RVM_FOLD_MIN_TOKENS: from this many tokens the router folds every logit in the reference's order
+# (exact logits, ids and weights); decode and smaller batches use the certified estimates.
+FOLD_MIN_TOKENS = 256
+
+
 class MoeLayer:
     """One layer's device weights (`rvm_layer`)."""
 

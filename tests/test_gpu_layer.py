@@ -82,7 +82,7 @@ def test_router_certified_ids_match_oracle(gpu, orc):
     for bias in (False, True):
         key = get_layer(0, bias=bias)
         L, router, b = key[0], key[1], key[2]
-        n = 1024
+        n = moe.FOLD_MIN_TOKENS - 1  # the certified path (larger batches fold every logit)
         x = synth.tokens(SEED + 1, n)
         ws = moe.Workspace(L, n)
         ids, w, lg = moe.router_select(L, dev(x), n, ws, with_logits=True)
@@ -107,7 +107,7 @@ def test_router_exact_candidates_match_the_full_exact_path(gpu, orc):
     for bias in (False, True):
         key = get_layer(0, bias=bias)
         L, router, b = key[0], key[1], key[2]
-        n = 1024
+        n = moe.FOLD_MIN_TOKENS - 1
         x = synth.tokens(SEED + 2, n)
         want_ids, want_w, _ = orc.select_experts(orc.router_logits(router, b, x, N_EXP, D), TOP_K)
         ws = moe.Workspace(L, n)
@@ -127,14 +127,36 @@ def test_router_ties_go_to_the_lower_index(gpu, orc):
     router[[7, 50, 51]] = router[3]          # identical logits: only the index can order them
     router[[90, 91]] = router[12]
     L = moe.MoeLayer(N_EXP, TOP_K, D, FF, router)
-    n = 256
-    x = synth.tokens(7, n)
+    for n in (moe.FOLD_MIN_TOKENS - 1, moe.FOLD_MIN_TOKENS):  # certified path, then the fold path
+        x = synth.tokens(7, n)
+        ws = moe.Workspace(L, n)
+        ids, w = moe.router_select(L, dev(x), n, ws)
+        want_ids, want_w, _ = orc.select_experts(orc.router_logits(router, None, x, N_EXP, D), TOP_K)
+        assert np.array_equal(ids, want_ids.astype(np.int32))
+        assert np.max(np.abs(w - want_w)) <= 1e-5
+        assert (ws.fallbacks() > 0) == (n < moe.FOLD_MIN_TOKENS)
+
+
+@pytest.mark.parametrize("n,bias,pre", [(256, False, False), (1000, True, False), (333, True, True)])
+def test_router_fold_path_is_the_references_bits(gpu, orc, n, bias, pre):
+    """From FOLD_MIN_TOKENS tokens every logit is folded in the reference's order: logits and ids
+    are the oracle's bit for bit (ragged last token tile, router bias, pre-norm); the weights
+    differ from the oracle's only through expf ((float)exp(double) on the device, the host libm's
+    expf in the oracle)."""
+    key = get_layer(0, bias=bias)
+    L, router, b = key[0], key[1], key[2]
+    x = synth.tokens(SEED + 11, n)
+    print(f"[fold] {n} tokens bias={bias} pre_norm={pre}", flush=True)
     ws = moe.Workspace(L, n)
-    ids, w = moe.router_select(L, dev(x), n, ws)
-    want_ids, want_w, _ = orc.select_experts(orc.router_logits(router, None, x, N_EXP, D), TOP_K)
+    flags = hip.PRE_NORM if pre else 0
+    ids, w, lg = moe.router_select(L, dev(x), n, ws, flags=flags, with_logits=True)
+    xin = np.stack([orc.rms_norm(r, None, 1e-6) for r in x]) if pre else x
+    want_lg = orc.router_logits(router, b, xin, N_EXP, D)
+    want_ids, want_w, _ = orc.select_experts(want_lg, TOP_K)
+    assert np.array_equal(lg, want_lg)
     assert np.array_equal(ids, want_ids.astype(np.int32))
-    assert np.max(np.abs(w - want_w)) <= 1e-5
-    assert ws.fallbacks() > 0
+    assert np.max(np.abs(w - want_w)) <= 2e-7
+    assert ws.fallbacks() == 0
 
 
 def test_plan_matches_oracle(gpu, orc):
@@ -222,7 +244,10 @@ def test_forward_batch_sizes_are_batch_invariant(gpu, n, extras):
         assert np.array_equal(o1.download(np.float32, D), got[t]), t
 
 
-def test_prefill_512_is_batch_invariant(gpu, orc):
+def test_prefill_512_matches_oracle_and_decode(gpu, orc):
+    """512 tokens take the fold path: ids are the oracle's bit for bit; each sampled
+    token has its single-token decode's ids, and its row agrees with the decode row (whose
+    weights come from the certified estimates) and with the oracle."""
     key = get_layer(0)
     L = key[0]
     n = 512
@@ -231,10 +256,15 @@ def test_prefill_512_is_batch_invariant(gpu, orc):
     xd, out = dev(x), DevBuf(n * D * 4)
     moe.forward(L, xd, out, n, ws)
     got = out.download(np.float32, n * D).reshape(n, D)
+    ids, w = ws.selection(L, n)
+    want_ids, want_w, _ = orc.select_experts(orc.router_logits(key[1], None, x, N_EXP, D), TOP_K)
+    assert np.array_equal(ids, want_ids.astype(np.int32))
+    assert np.max(np.abs(w - want_w)) <= 2e-7
     ws1, o1 = moe.Workspace(L, 1), DevBuf(D * 4)
     for t in range(0, n, 37):
         moe.decode(L, xd, o1, ws1, x_off=t * D * 4)
-        assert np.array_equal(o1.download(np.float32, D), got[t]), t
+        assert np.array_equal(ws1.selection(L, 1)[0][0], ids[t]), t
+        assert_close(o1.download(np.float32, D), got[t], f"decode row {t}")
     sub = [0, 255, 511]
     _, _, out_ref, _ = oracle_layer(orc, key, x[sub])
     for i, t in enumerate(sub):
