@@ -17,6 +17,7 @@
 #pragma once
 #include <math.h>
 
+#include "expf.hpp"
 #include "internal.hpp"
 
 namespace rvm {
@@ -150,8 +151,8 @@ __device__ __forceinline__ void wave_top_k(const uint32_t (&k)[4], bool (&alive)
 }
 
 // The reference's selection from its exact logits, one wave (runtime/src/exec.rs:507-517):
-// softmax (runtime/src/ops.rs:170-179: max ignoring NaN, numerators expf(R - max) correctly
-// rounded, their f64 sum in index order, inv = (1/sum) as f32, p * inv), top_k by total_cmp with
+// softmax (runtime/src/ops.rs:170-179: max ignoring NaN, numerators expf(R - max) as glibc's expf,
+// their f64 sum in index order, inv = (1/sum) as f32, p * inv), top_k by total_cmp with
 // ties to the lower index (ops.rs:182-187), and the weights p_j / max(sum of the selected p in top
 // order, 2^-14). R[i] is expert lane + 64 i (-inf past n_exp); sp (256 floats), sel and wsel are
 // LDS of this wave; lg_t, when set, receives the logits. Every lane of the wave calls this.
@@ -166,7 +167,7 @@ __device__ __forceinline__ void exact_softmax_top_k(const float (&R)[4], int n_e
             if (lane + 64 * i < n_exp) lg_t[lane + 64 * i] = R[i];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        if (lane + 64 * i < n_exp) sp[lane + 64 * i] = (float)exp((double)(R[i] - Mf));
+        if (lane + 64 * i < n_exp) sp[lane + 64 * i] = glibc_expf(R[i] - Mf);
     wave_lds_sync();
     float inv = 0.0f;
     if (lane == 0) {
@@ -446,7 +447,7 @@ __device__ bool exact_candidates(SelShared<F4, NW> &sh, const float *__restrict_
         const int ce = sh.cand[min(lane, nc - 1)];
         const float R = bias ? acc + bias[ce] : acc;
         const float Mf = wave_max_f(lane < nc ? R : -INFINITY);  // the largest logit is a candidate's
-        const float spc = (float)exp((double)(R - Mf));         // exactly the reference's numerator
+        const float spc = glibc_expf(R - Mf);                   // exactly the reference's numerator
         // rank of each candidate by (numerator desc, index asc); the candidates are in index order
         if (lane < nc) sh.csp[lane] = spc;
         wave_lds_sync();
@@ -478,7 +479,7 @@ __device__ bool exact_candidates(SelShared<F4, NW> &sh, const float *__restrict_
             const int e = lane + 64 * i;
             if (e < n_exp && !((cmask[i] >> lane) & 1ull)) {
                 const float hi = round_up_f32(sh.Sx[e] + sh.Ex[e]);
-                ok = ok && (float)exp((double)(hi - Mf)) * sep < pk;
+                ok = ok && glibc_expf(hi - Mf) * sep < pk;
             }
         }
         ok = __ballot(!ok) == 0;

@@ -96,7 +96,7 @@ def test_router_certified_ids_match_oracle(gpu, orc):
         ids2, w2, lg2 = moe.router_select(L, dev(x), n, ws2, flags=hip.EXACT_SELECT, with_logits=True)
         assert np.array_equal(lg2, want_lg)
         assert np.array_equal(ids2, want_ids.astype(np.int32))
-        assert np.max(np.abs(w2 - want_w)) <= 2e-7
+        assert np.array_equal(w2, want_w)
         assert ws2.fallbacks() == n
 
 
@@ -139,10 +139,8 @@ def test_router_ties_go_to_the_lower_index(gpu, orc):
 
 @pytest.mark.parametrize("n,bias,pre", [(256, False, False), (1000, True, False), (333, True, True)])
 def test_router_fold_path_is_the_references_bits(gpu, orc, n, bias, pre):
-    """From FOLD_MIN_TOKENS tokens every logit is folded in the reference's order: logits and ids
-    are the oracle's bit for bit (ragged last token tile, router bias, pre-norm); the weights
-    differ from the oracle's only through expf ((float)exp(double) on the device, the host libm's
-    expf in the oracle)."""
+    """From FOLD_MIN_TOKENS tokens every logit is folded in the reference's order: logits, ids
+    and weights are the oracle's bit for bit (ragged last token tile, router bias, pre-norm)."""
     key = get_layer(0, bias=bias)
     L, router, b = key[0], key[1], key[2]
     x = synth.tokens(SEED + 11, n)
@@ -155,7 +153,7 @@ def test_router_fold_path_is_the_references_bits(gpu, orc, n, bias, pre):
     want_ids, want_w, _ = orc.select_experts(want_lg, TOP_K)
     assert np.array_equal(lg, want_lg)
     assert np.array_equal(ids, want_ids.astype(np.int32))
-    assert np.max(np.abs(w - want_w)) <= 2e-7
+    assert np.array_equal(w, want_w)
     assert ws.fallbacks() == 0
 
 
@@ -245,7 +243,7 @@ def test_forward_batch_sizes_are_batch_invariant(gpu, n, extras):
 
 
 def test_prefill_512_matches_oracle_and_decode(gpu, orc):
-    """512 tokens take the fold path: ids are the oracle's bit for bit; each sampled
+    """512 tokens take the fold path: ids, weights and outputs are the oracle's bit for bit; each sampled
     token has its single-token decode's ids, and its row agrees with the decode row (whose
     weights come from the certified estimates) and with the oracle."""
     key = get_layer(0)
@@ -259,7 +257,7 @@ def test_prefill_512_matches_oracle_and_decode(gpu, orc):
     ids, w = ws.selection(L, n)
     want_ids, want_w, _ = orc.select_experts(orc.router_logits(key[1], None, x, N_EXP, D), TOP_K)
     assert np.array_equal(ids, want_ids.astype(np.int32))
-    assert np.max(np.abs(w - want_w)) <= 2e-7
+    assert np.array_equal(w, want_w)
     ws1, o1 = moe.Workspace(L, 1), DevBuf(D * 4)
     for t in range(0, n, 37):
         moe.decode(L, xd, o1, ws1, x_off=t * D * 4)
@@ -269,6 +267,7 @@ def test_prefill_512_matches_oracle_and_decode(gpu, orc):
     _, _, out_ref, _ = oracle_layer(orc, key, x[sub])
     for i, t in enumerate(sub):
         assert_close(got[t], out_ref[i], f"token {t}")
+        assert np.array_equal(got[t], out_ref[i]), f"token {t}: not the oracle's bits"
 
 
 def test_graph_replays_match_eager(gpu):
