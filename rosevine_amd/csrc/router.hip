@@ -185,12 +185,12 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void k_select(const double2 *__rest
 // of a wave is token t0 + l, the wave's expert is uniform, and each lane adds the f32 products
 // W_r[e][i] * x'[i] in element order from -0.0 (runtime/src/ops.rs:321-326), then the bias, so the
 // logits are the reference's bit for bit. The tile's 64 tokens are staged in LDS FKC columns at a
-// time (double-buffered, the next chunk's loads in flight), with the workgroup's router rows beside
-// them, read as LDS broadcasts (every wait in the loop is then on in-order LDS traffic; scalar loads
-// share the LDS wait counter and complete out of order, and taking the row from lanes with
-// v_readlane measured slower). Column quad q of token t sits at [q][t ^ (q & 7)], so the coalesced
-// stores (eight quads of one token) and the per-token reads (one quad of 64 tokens) are free of
-// bank conflicts. Workgroup g also
+// time (double-buffered, the next chunk's loads in flight). The wave's router row comes through
+// scalar loads, 64 floats at a time: scalar loads share the LDS wait counter and complete out of
+// order, so each batch costs one wait on everything in flight, and larger batches spill scalar
+// registers (rows as LDS broadcasts, or taken from lanes with v_readlane, measured slower). Column
+// quad q of token t sits at [q][t ^ (q & 7)], so the coalesced stores (eight quads of one token) and
+// the per-token reads (one quad of 64 tokens) are free of bank conflicts. Workgroup g also
 // quantises the Q8_0 blocks of tokens g, g + gridDim.x, ... of each staged chunk
 // (runtime/src/ops.rs:95-105).
 constexpr int FOLD_MIN_TOKENS = RVM_FOLD_MIN_TOKENS;
@@ -217,27 +217,24 @@ __global__ __launch_bounds__(FW * 64) void k_router_fold(const float *__restrict
                                                          float *__restrict__ xsc) {
     constexpr int d = 256 * F4, nb = d / QK, NCH = d / FKC, KQ = FKC / 4, LD = 64 * KQ / (FW * 64);
     static_assert(d % FKC == 0 && FKC % QK == 0 && KQ % 4 == 0, "whole blocks per chunk");
-    static_assert(FW * KQ <= FW * 64, "one row quad per thread");
     __shared__ float4 xs[2][KQ][64];  // the tile's layer input, column quad q of token t at [q][t ^ (q & 7)]
-    __shared__ float4 wsh[2][FW][KQ];  // the workgroup's router rows
     __shared__ float sc[64];
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int t0 = blockIdx.y * 64;
     const int ew = blockIdx.x * FW + w;
     if (tid < 64) sc[tid] = scale ? scale[min(t0 + tid, n_tok - 1)] : 1.0f;
-    // staging: thread tid moves quad (tid % KQ) of tokens tid / KQ + j (256 / KQ), j < LD, and
-    // threads below FW KQ quad (tid % KQ) of row tid / KQ
+    // staging: thread tid moves quad (tid % KQ) of tokens tid / KQ + j (256 / KQ), j < LD
     const int sq = tid % KQ, st = tid / KQ;
-    const bool wst = tid < FW * KQ;
     const float *xrow[LD];
 #pragma unroll
     for (int j = 0; j < LD; ++j) xrow[j] = x + (size_t)min(t0 + st + j * (256 / KQ), n_tok - 1) * d + 4 * sq;
-    const float *wrow = W + (size_t)min(blockIdx.x * FW + (wst ? st : 0), n_exp - 1) * d + 4 * sq;
-    float4 pf[LD], pw;
+    // the wave's row through the constant address space: uniform loads there are scalar loads
+    typedef const __attribute__((address_space(4))) float *cfloatp;
+    const cfloatp wsrow = (cfloatp)(uintptr_t)(W + (size_t)__builtin_amdgcn_readfirstlane(min(ew, n_exp - 1)) * d);
+    float4 pf[LD];
 #pragma unroll
     for (int j = 0; j < LD; ++j) pf[j] = *(const float4 *)xrow[j];
-    pw = *(const float4 *)wrow;
     __syncthreads();  // sc
     auto stage = [&](int buf) {
 #pragma unroll
@@ -247,7 +244,6 @@ __global__ __launch_bounds__(FW * 64) void k_router_fold(const float *__restrict
             const float4 v = scale ? make_float4(pf[j].x * s, pf[j].y * s, pf[j].z * s, pf[j].w * s) : pf[j];
             xs[buf][sq][tt ^ (sq & 7)] = v;
         }
-        if (wst) wsh[buf][st][sq] = pw;
     };
     stage(0);
     __syncthreads();
@@ -262,22 +258,24 @@ __global__ __launch_bounds__(FW * 64) void k_router_fold(const float *__restrict
         const int cn = min(c + 1, NCH - 1);
 #pragma unroll
         for (int j = 0; j < LD; ++j) pf[j] = *(const float4 *)(xrow[j] + cn * FKC);
-        pw = *(const float4 *)(wrow + cn * FKC);
-        // 4 quads at a time (the row quad is the same address in every lane: a broadcast)
-#pragma unroll 2
-        for (int q0 = 0; q0 < KQ; q0 += 4) {
-            float4 wv[4], xv[4];
+        // the row in scalar registers, half a chunk (64 floats) at a time: one wait on the scalar
+        // loads per half, then only LDS reads are in flight and their waits are exact
+#pragma unroll 1
+        for (int h = 0; h < 2; ++h) {
+            float4 wv[KQ / 2];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                wv[q] = wsh[buf][w][q0 + q];
-                xv[q] = xs[buf][q0 + q][lane ^ ((q0 + q) & 7)];
+            for (int q = 0; q < KQ / 2; ++q) {
+                const int o = 4 * (c * KQ + h * (KQ / 2) + q);
+                wv[q] = make_float4(wsrow[o], wsrow[o + 1], wsrow[o + 2], wsrow[o + 3]);
             }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                acc = acc + wv[q].x * xv[q].x;
-                acc = acc + wv[q].y * xv[q].y;
-                acc = acc + wv[q].z * xv[q].z;
-                acc = acc + wv[q].w * xv[q].w;
+            for (int q = 0; q < KQ / 2; ++q) {
+                const int qq = h * (KQ / 2) + q;
+                const float4 v = xs[buf][qq][lane ^ (qq & 7)];
+                acc = acc + wv[q].x * v.x;
+                acc = acc + wv[q].y * v.y;
+                acc = acc + wv[q].z * v.z;
+                acc = acc + wv[q].w * v.w;
             }
         }
         for (int jp = 2 * w; jp < njobs; jp += 2 * FW) {
