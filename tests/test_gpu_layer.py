@@ -270,6 +270,27 @@ def test_prefill_512_matches_oracle_and_decode(gpu, orc):
         assert np.array_equal(got[t], out_ref[i]), f"token {t}: not the oracle's bits"
 
 
+def test_forward_fold_path_ragged_pre_norm_matches_oracle_bitwise(gpu, orc):
+    """300 tokens (a ragged last tile of 44) with pre-norm, router bias and down scales: the fold
+    path's Q8_0 blocks of the normed input (formed by the router fold, token g of each tile by
+    workgroup g) feed the experts, and the first and last tokens of every tile are the oracle's
+    bits."""
+    key = get_layer(0, bias=True, ds=True)
+    L = key[0]
+    n = 300
+    x = synth.tokens(SEED + 12, n)
+    print(f"[fold forward] {n} tokens pre_norm bias ds", flush=True)
+    ws = moe.Workspace(L, n)
+    xd, out = dev(x), DevBuf(n * D * 4)
+    moe.forward(L, xd, out, n, ws, flags=hip.PRE_NORM)
+    got = out.download(np.float32, n * D).reshape(n, D)
+    sub = [0, 63, 64, 127, 191, 255, 256, 299]
+    _, _, out_ref, _ = oracle_layer(orc, key, x[sub], pre_norm=True)
+    for i, t in enumerate(sub):
+        assert_close(got[t], out_ref[i], f"token {t}")
+        assert np.array_equal(got[t], out_ref[i]), f"token {t}: not the oracle's bits"
+
+
 def test_graph_replays_match_eager(gpu):
     key = get_layer(0)
     L = key[0]
