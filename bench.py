@@ -30,13 +30,31 @@ METRIC = "MoE-layer decode tokens/s + achieved HBM GB/s (% of peak), batch 1"
 HBM_PEAK_GBS = 8000.0
 EXPERT_BYTES = 2816 // 32 * 18 * 1408 + 704 // 32 * 18 * 2816  # 3,345,408
 ROUTER_BYTES = 128 * 2816 * 4  # 1,441,792
-# HBM bytes one decode call moves (read + written), from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
-# this workload calibrated against a device copy of known size (profiles/decode_hbm_traffic.md).
+# HBM bytes one decode call moves (read + written): rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
+# this workload, each calibrated against a device copy of known size. The counters cannot be read
+# from inside this process, so the figure is the profile's, named in the line.
 MEASURED_TRAFFIC = 33_684_001
+TRAFFIC_SOURCE = "profiles/decode_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE passes)"
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def host_cpu() -> dict:
+    """The host CPU's model name (as lscpu prints it, from /proc/cpuinfo), its logical CPU count
+    and the CPUs this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return {"model": model, "cpus": os.cpu_count() or 1, "usable": usable}
 
 
 def cpu_baseline(seed: int, n_tokens: int, seconds: float, threads: int):
@@ -65,9 +83,14 @@ def cpu_baseline(seed: int, n_tokens: int, seconds: float, threads: int):
         done += 1
     dt = time.perf_counter() - t0
     pool.close()
+    host = host_cpu()
     return {"value": round(done / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{done} decode tokens of the same workload in {dt:.1f} s "
-                      f"({'avx2_q8' if orc.CpuBaseline.uses_avx2() else 'scalar'} kernel, {threads} threads)"}
+                      f"({'avx2_q8' if orc.CpuBaseline.uses_avx2() else 'scalar'} kernel, {threads} threads)",
+            "cpu_model": host["model"], "host_cpus": host["cpus"], "usable_cpus": host["usable"],
+            "cores_note": f"{threads} worker threads: the GPU host's CPU share for one GPU is 16 threads, "
+                          f"whatever nproc reports ({host['usable']} here)" if threads < host["usable"] else
+                          "every usable host core"}
 
 
 def _timed(run, iters: int, warm: int):
@@ -83,6 +106,56 @@ def _timed(run, iters: int, warm: int):
     e1.record()
     e1.synchronize()
     return e0.elapsed_ms(e1) / iters
+
+
+def measure_stack30(seed: int, n_layers: int = 30, n_tok: int = 40):
+    """Single-token decode through n_layers seeded layers (router bias N(0,1), RMSNorm eps 1e-6 of
+    the previous output as the input from layer 1 on), captured in HIP graphs on the current
+    stream: (ms per token after 4 warm-up tokens, resident expert bytes). The layers' 12.9 GB of
+    experts do not fit the last-level cache, so every token reads its experts from HBM."""
+    from rosevine_amd import hip, moe, synth
+
+    E, K8, D, FF = synth.N_EXP, synth.TOP_K, synth.D, synth.FF
+    layers = []
+    for l in range(n_layers):
+        ly = moe.MoeLayer(E, K8, D, FF, synth.router_weights(seed, l), synth.router_bias(seed, l))
+        ly.synth_weights(seed, synth.gate_up_stream(l), synth.down_stream(l))
+        layers.append(ly)
+    hip.sync()
+    stream = hip.Stream()
+    stream.use()
+    ws = moe.Workspace(layers[0], 1)
+    x = hip.DevBuf.from_array(synth.tokens(seed + 300, n_tok))
+    bufs = [hip.DevBuf(D * 4) for _ in range(2)]
+    nb = D * 4
+
+    def capture(t0: int, n: int) -> hip.Graph:
+        hip.Graph.begin()
+        for t in range(t0, t0 + n):
+            moe.decode(layers[0], x, bufs[0], ws, x_off=t * nb)
+            for l in range(1, n_layers):  # the next layer's input is rms_norm(previous output, eps 1e-6)
+                moe.decode(layers[l], bufs[(l - 1) % 2], bufs[l % 2], ws, flags=hip.PRE_NORM)
+        return hip.Graph.end()
+
+    warm, timed = capture(0, 4), capture(4, n_tok - 4)
+    warm.launch()
+    hip.sync()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record()
+    timed.launch()
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / (n_tok - 4)
+    warm.close()
+    timed.close()
+    hip.Stream.use_default()
+    stream.close()
+    resident = n_layers * layers[0].weight_bytes
+    for ly in layers:
+        for b in (ly.gate_up, ly.down, ly.router, ly.bias):
+            if b is not None:
+                b.close()
+    return ms, resident
 
 
 def other_workload(args) -> int:
@@ -261,43 +334,15 @@ def other_workload(args) -> int:
                                   "bytes_per_step": nbytes}})
     else:  # stack30
         L = 30
-        layers = []
-        for l in range(L):
-            ly = moe.MoeLayer(E, K8, D, FF, synth.router_weights(args.seed, l), synth.router_bias(args.seed, l))
-            ly.synth_weights(args.seed, synth.gate_up_stream(l), synth.down_stream(l))
-            layers.append(ly)
-        hip.sync()
-        ws = moe.Workspace(layers[0], 1)
         n_tok = 40
-        x = hip.DevBuf.from_array(synth.tokens(args.seed + 300, n_tok))
-        bufs = [hip.DevBuf(D * 4) for _ in range(2)]
-        nb = D * 4
-
-        def capture(t0: int, n: int) -> hip.Graph:
-            hip.Graph.begin()
-            for t in range(t0, t0 + n):
-                moe.decode(layers[0], x, bufs[0], ws, x_off=t * nb)
-                for l in range(1, L):  # the next layer's input is rms_norm(previous output, eps 1e-6)
-                    moe.decode(layers[l], bufs[(l - 1) % 2], bufs[l % 2], ws, flags=hip.PRE_NORM)
-            return hip.Graph.end()
-
-        warm, timed = capture(0, 4), capture(4, n_tok - 4)
-        warm.launch()
-        hip.sync()
-        e0, e1 = hip.Event(), hip.Event()
-        e0.record()
-        timed.launch()
-        e1.record()
-        e1.synchronize()
-        ms = e0.elapsed_ms(e1) / (n_tok - 4)
-        warm.close()
-        timed.close()
+        ms, resident = measure_stack30(args.seed, L, n_tok)
         nbytes = L * (K8 * EXPERT_BYTES + ROUTER_BYTES)
         line.update({"metric": "30-layer MoE stack decode tokens/s, batch 1", "value": round(1e3 / ms, 1),
                      "unit": "tokens/s", "steps": n_tok - 4, "warmup": 4, "ms_per_step": round(ms, 6),
                      "scaling": "weak",
-                     "config": {"workload": "stack30", "layers": L, "resident_bytes": L * layers[0].weight_bytes,
-                                "routing": "per-expert bias N(0,1)", "norm": "RMSNorm eps 1e-6 between layers"},
+                     "config": {"workload": "stack30", "layers": L, "resident_bytes": resident,
+                                "routing": "per-expert bias N(0,1)", "norm": "RMSNorm eps 1e-6 between layers",
+                                "us_per_layer": round(ms * 1e3 / L, 3)},
                      "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms / 1e3) / 1e9, 1),
                                   "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                   "frac": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -316,6 +361,7 @@ def main() -> int:
     ap.add_argument("--graph-chunk", type=int, default=500, help="tokens per captured graph")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 30-layer (cache-cold) context figure")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--workload", default="decode", choices=["decode", "prefill512", "ragged32", "stack30", "q4gemv", "attn"],
                     help="decode (default, the headline line); prefill512: one layer over 512 tokens; ragged32: "
@@ -403,9 +449,20 @@ def main() -> int:
     log(f"[bench] {ms_per_step * 1e3:.2f} us/token, {tok_s:.0f} tokens/s, {achieved:.0f} GB/s, "
         f"router fallbacks {fallbacks}/{K}")
 
+    stack = None
+    if not args.no_stack:
+        log("[bench] 30-layer stack (cache-cold context)")
+        s30, resident = measure_stack30(args.seed)
+        stack = {"us_per_token": round(s30 * 1e3, 2), "us_per_layer": round(s30 * 1e3 / 30, 3),
+                 "layers": 30, "resident_bytes": resident,
+                 "frac_of_hbm_peak": round(30 * bytes_tok / (s30 / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                 "note": "config 3: single-token decode through 30 layers (router bias, RMSNorm between "
+                         "layers), 12.9 GB of experts, none of it held in the 256 MB last-level cache"}
+        log(f"[bench] stack30: {stack['us_per_layer']} us per layer")
+
     cpu = None
     if not args.no_cpu:
-        threads = max(1, min(os.cpu_count() or 1, 16))
+        threads = max(1, min(host_cpu()["usable"], 16))
         log(f"[bench] CPU baseline on {threads} threads for up to {args.cpu_seconds} s")
         cpu = cpu_baseline(args.seed, 100000, args.cpu_seconds, threads)
 
@@ -422,13 +479,18 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int4xint8->int32, f32",
         "data": "synthetic (seeded Q4_0 experts, N(0,1) tokens, N(0,0.02) router)",
-        "config": {"workload": "single MoE layer, batch-1 decode, 10k back-to-back tokens, iid routing",
+        "config": {"workload": f"single MoE layer, batch-1 decode, {K} back-to-back tokens timed after {W} "
+                               "warm-up tokens, each a fresh x ~ N(0, 1), iid routing",
                    "n_exp": synth.N_EXP, "top_k": synth.TOP_K, "d": synth.D, "ff": synth.FF,
                    "tokens": K, "graph_tokens": ch, "router_fallbacks": fallbacks},
         "roofline": {"bound": "hbm", "kernel": "rvm_moe_decode (k_router + k_gateup_decode + k_down_fold)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC,
-                     "bytes_per_launch": bytes_tok},
+                     "traffic_source": TRAFFIC_SOURCE, "bytes_per_launch": bytes_tok,
+                     "cache_note": "one layer's 428 MB of experts against MI355X's 256 MB last-level cache: "
+                                   "part of each token's expert bytes hit that cache; stack30 reads 12.9 GB "
+                                   "and is the cache-cold figure"},
+        "stack30": stack,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -13,69 +13,11 @@ what the oracle is too slow to check in full.
 import numpy as np
 import pytest
 
+from layer_util import D, FF, N_EXP, SEED, TOP_K, HostExperts, assert_close, dev, get_layer, oracle_layer
 from rosevine_amd import hip, moe, synth
 from rosevine_amd.hip import DevBuf
 
 pytestmark = pytest.mark.gpu
-
-N_EXP, TOP_K, D, FF = synth.N_EXP, synth.TOP_K, synth.D, synth.FF
-SEED = 0
-
-
-def dev(a):
-    return DevBuf.from_array(np.ascontiguousarray(a))
-
-
-def rms(a):
-    return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
-
-
-def assert_close(got, want, what):
-    err, r = float(np.max(np.abs(got - want))), rms(want)
-    assert err <= 1e-3 * r, f"{what}: max|diff| {err:.3g} > 1e-3 * rms {r:.3g}"
-    assert err <= 2e-5 * r, f"{what}: max|diff| {err:.3g} > 2e-5 * rms {r:.3g}"
-
-
-class HostExperts(dict):
-    """Reference-layout Q4_0 experts regenerated on the host on first use."""
-
-    def __init__(self, seed, stream0, n_out, k):
-        super().__init__()
-        self.args = (seed, stream0, n_out, k)
-
-    def __missing__(self, e):
-        seed, stream0, n_out, k = self.args
-        v = synth.host_expert(seed, stream0, int(e), n_out, k)
-        self[e] = v
-        return v
-
-
-_layers = {}
-
-
-def get_layer(layer=0, bias=False, ds=False):
-    key = (layer, bias, ds)
-    if key not in _layers:
-        router = synth.router_weights(SEED, layer)
-        b = synth.router_bias(SEED, layer) if bias else None
-        dsc = np.random.default_rng([SEED, layer, 9]).uniform(0.5, 1.5, N_EXP).astype(np.float32) if ds else None
-        L = moe.MoeLayer(N_EXP, TOP_K, D, FF, router, b, dsc)
-        L.synth_weights(SEED, synth.gate_up_stream(layer), synth.down_stream(layer))
-        gu = HostExperts(SEED, synth.gate_up_stream(layer), 2 * FF, D)
-        dn = HostExperts(SEED, synth.down_stream(layer), D, FF)
-        _layers[key] = (L, router, b, dsc, gu, dn)
-    return _layers[key]
-
-
-def oracle_layer(orc, key, x, pre_norm=False):
-    L, router, b, dsc, gu, dn = key
-    xin = np.stack([orc.rms_norm(r, None, 1e-6) for r in x]) if pre_norm else x
-    lg = orc.router_logits(router, b, xin, N_EXP, D)
-    ids, w, _ = orc.select_experts(lg, TOP_K)
-    for e in set(int(v) for v in ids.reshape(-1)):
-        gu[e], dn[e]
-    out = orc.experts_q8(gu, dn, dsc, xin, D, FF, ids, w, N_EXP)
-    return ids, w, out, lg
 
 
 def test_router_certified_ids_match_oracle(gpu, orc):
@@ -188,9 +130,9 @@ def test_decode_matches_oracle(gpu, orc, bias, ds, pre):
     flags = hip.PRE_NORM if pre else 0
     for t in range(n):
         moe.decode(L, xd, out, ws, flags=flags, x_off=t * D * 4, out_off=t * D * 4)
+        ids_dev = ws.selection(L, 1)[0][0]
+        assert np.array_equal(ids_dev, ids_ref[t].astype(np.int32)), t
     got = out.download(np.float32, n * D).reshape(n, D)
-    ids_dev = ws.selection(L, 1)[0][0]  # last token's selection
-    assert np.array_equal(ids_dev, ids_ref[-1].astype(np.int32))
     for t in range(n):
         assert_close(got[t], out_ref[t], f"token {t}")
 
