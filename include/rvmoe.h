@@ -176,6 +176,17 @@ int rvm_moe_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int
 int rvm_moe_decode(const rvm_layer *layer, const float *x, float *out, int flags, float eps, void *ws,
                    size_t ws_bytes);
 
+/* rvm_moe_decode without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. Its scratch is a static device array of RVM_STATIC_SCRATCH_BYTES
+ * in the library, one per GPU, held until the process ends; its address is taken by rvh_init (or
+ * by the first call on a device) and the call allocates nothing. Every supported layer shape fits
+ * (the largest, 256 experts, top-8, d = 4096, ff = 1024, needs about 8.1 MiB); a layer that needed
+ * more would be refused with hipErrorInvalidValue. Calls on one GPU share the array: calls that
+ * overlap on one GPU (two streams, or two host threads) race. */
+#define RVM_STATIC_SCRATCH_BYTES (9u << 20)
+int rvm_moe_decode_static(const rvm_layer *layer, const float *x, float *out, int flags, float eps);
+
 /* n_tok tokens through one MoE layer with device grouping (ragged decode batches and prefill). */
 int rvm_moe_forward(const rvm_layer *layer, const float *x, float *out, int n_tok, int flags, float eps, void *ws,
                     size_t ws_bytes);

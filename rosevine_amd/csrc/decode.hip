@@ -15,6 +15,8 @@
 //      in block order and combines the slots in slot order.
 // Every lane issues all of its 16-byte weight loads before the first use, the activation blocks
 // are staged once per workgroup in LDS, and each wave reads its blocks from LDS in one burst.
+#include <mutex>
+
 #include "select.hpp"
 
 namespace rvm {
@@ -270,8 +272,10 @@ __global__ __launch_bounds__(256) void k_down_fold(const float *__restrict__ dte
 
 using namespace rvm;
 
-extern "C" int rvm_moe_decode(const rvm_layer *L, const float *x, float *out, int flags, float eps, void *ws,
-                              size_t ws_bytes) {
+namespace {
+
+// One decode token through the layer, scratch in ws (ws_layout(L, 1) bytes).
+int moe_decode(const rvm_layer *L, const float *x, float *out, int flags, float eps, void *ws, size_t ws_bytes) {
     RVM_CHECK(layer_ok(L) && x && out && ws);
     const WsLayout lay = ws_layout(L, 1);
     RVM_CHECK(ws_bytes >= lay.total);
@@ -303,4 +307,60 @@ extern "C" int rvm_moe_decode(const rvm_layer *L, const float *x, float *out, in
                            L->down_scale, out, L->d, L->top_k);
         return launched();
     });
+}
+
+
+// ---- The workspace-free decode (rvm_moe_decode_static) ----
+// Its scratch is this array: one copy per GPU, loaded with the library's code object and held until
+// the process ends. Host code uses the array's per-device address (hipGetSymbolAddress, taken once
+// per device with that device current), never the array's name, which on the host is only a stand-in.
+// No word of it must start at zero: every word a decode call reads was written earlier in that call
+// (the fallback counter at offset 0 counts across calls and no kernel reads it).
+static __device__ __align__(256) uint8_t scratch[RVM_STATIC_SCRATCH_BYTES];
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[MAX_DEVICES];
+
+}  // namespace
+
+namespace rvm {
+
+// Takes the scratch array's address on `device`, which must be current; idempotent.
+int static_scratch_setup(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[device]) return 0;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return (int)hipErrorInvalidSymbol;
+    g_scratch[device] = p;
+    return 0;
+}
+
+}  // namespace rvm
+
+extern "C" int rvm_moe_decode(const rvm_layer *L, const float *x, float *out, int flags, float eps, void *ws,
+                              size_t ws_bytes) {
+    return moe_decode(L, x, out, flags, eps, ws, ws_bytes);
+}
+
+extern "C" int rvm_moe_decode_static(const rvm_layer *L, const float *x, float *out, int flags, float eps) {
+    RVM_CHECK(layer_ok(L) && x && out);
+    const size_t need = ws_layout(L, 1).total;
+    if (need > RVM_STATIC_SCRATCH_BYTES) return (int)hipErrorInvalidValue;
+    int dev = 0;
+    RVM_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= MAX_DEVICES) return (int)hipErrorInvalidDevice;
+    void *ws = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        ws = g_scratch[dev];
+    }
+    if (!ws) {
+        if (int rc = static_scratch_setup(dev)) return rc;
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        ws = g_scratch[dev];
+    }
+    return moe_decode(L, x, out, flags, eps, ws, need);
 }

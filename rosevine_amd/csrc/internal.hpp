@@ -313,6 +313,9 @@ inline int with_steps(int n, F &&f) {
 
 // Device limits read once per process (rvh_init).
 int max_lds_per_block();
+// The per-device address of rvm_moe_decode_static's scratch array, taken once per device with
+// that device current (decode.hip; rvh_init calls it).
+int static_scratch_setup(int device);
 
 // Kernel launchers shared across translation units.
 // k_router (logit statistics and the Q8_0 input), then k_select unless select is false.

@@ -140,7 +140,7 @@ int rvh_init(int device) {
     if (e != hipSuccess) return (int)e;
     // The kernels are wave64 code for CDNA: refuse any other wave size instead of misbehaving.
     if (prop.warpSize != 64) return (int)hipErrorInvalidDevice;
-    return 0;
+    return rvm::static_scratch_setup(device);
 }
 
 int rvh_mem_info(size_t *free_bytes, size_t *total_bytes) {

@@ -107,6 +107,7 @@ SIGNATURES = {
     "rvm_router_select": (_i, [_PL, _vp, _i, _i, _f, _vp, _vp, _vp, _vp, _sz]),
     "rvm_moe_plan": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "rvm_moe_decode": (_i, [_PL, _vp, _vp, _i, _f, _vp, _sz]),
+    "rvm_moe_decode_static": (_i, [_PL, _vp, _vp, _i, _f]),
     "rvm_moe_forward": (_i, [_PL, _vp, _vp, _i, _i, _f, _vp, _sz]),
 }
 

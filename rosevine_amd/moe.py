@@ -106,6 +106,14 @@ def decode(layer: MoeLayer, x: DevBuf, out: DevBuf, ws: Workspace, flags: int = 
                                ws.nbytes))
 
 
+def decode_static(layer: MoeLayer, x: DevBuf, out: DevBuf, flags: int = 0, eps: float = 1e-6, x_off: int = 0,
+                  out_off: int = 0) -> None:
+    """One token with the library's static scratch instead of a workspace (rvm_moe_decode_static):
+    the call allocates nothing; calls that overlap on one GPU race."""
+    nb = layer.d * 4
+    check(lib().rvm_moe_decode_static(layer.ptr(), x.at(x_off, nb), out.at(out_off, nb), flags, eps))
+
+
 def forward(layer: MoeLayer, x: DevBuf, out: DevBuf, n_tok: int, ws: Workspace, flags: int = 0,
             eps: float = 1e-6) -> None:
     """n_tok tokens with device grouping (rvm_moe_forward)."""
