@@ -176,6 +176,31 @@ int rvm_moe_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int
 int rvm_moe_decode(const rvm_layer *layer, const float *x, float *out, int flags, float eps, void *ws,
                    size_t ws_bytes);
 
+/* The MoE block's two inputs from one hidden row o, as the reference's executor forms them
+ * (runtime/src/hip_exec.rs:784-796; on the CPU runtime/src/exec.rs:465-468 and 493-503). With
+ * s = 1 / sqrt(mean(o^2) + eps) (runtime/src/ops.rs:131-139):
+ *   router input  ((o[i] * s) * router_post) * router_scale[i]   (ffn_gate_inp.scale; post = 1/sqrt(d))
+ *   expert input  (o[i] * s) * expert_scale[i]                  (pre_ffw_norm_2.weight)
+ * each product rounded in that order; a NULL scale is no factor. */
+typedef struct rvm_block_norms {
+    float eps;
+    float router_post;
+    const float *router_scale; /* [d] or NULL */
+    const float *expert_scale; /* [d] or NULL */
+} rvm_block_norms;
+
+/* The reference's MoE block in one call per layer: the router norm and GEMV, the selection, the
+ * expert-input norm, the expert dispatch and the combine of runtime/src/hip_exec.rs:784-842
+ * (rvh_rms_norm(o, router_x, gate_inp_scale, eps, 1/sqrt(d)), rvh_f32_mm, the host's
+ * select_experts, rvh_rms_norm(o, moe_in, pre_ffw_norm_2, eps, 1), the experts and rvh_moe_combine),
+ * with no host round trip. out receives the combined expert output, before the post_ffw_norm_2
+ * norm the reference applies next (hip_exec.rs:845, an rvh_rms_norm call). flags: 0 or
+ * RVM_EXACT_SELECT. Decode is one token; forward takes n_tok tokens with device grouping. */
+int rvm_moe_block_decode(const rvm_layer *layer, const rvm_block_norms *norms, const float *o, float *out, int flags,
+                         void *ws, size_t ws_bytes);
+int rvm_moe_block_forward(const rvm_layer *layer, const rvm_block_norms *norms, const float *o, float *out, int n_tok,
+                          int flags, void *ws, size_t ws_bytes);
+
 /* rvm_moe_decode without a workspace argument, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
  * counterpart in the reference. Its scratch is a static device array of RVM_STATIC_SCRATCH_BYTES

@@ -160,7 +160,7 @@ template <int PER>  // steps per wave = (d / 32) / GU_WAVES = d / 256
 __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
     const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl, const uint4 *__restrict__ dnib,
     const uint16_t *__restrict__ dscl, const double2 *__restrict__ stats, const float *__restrict__ bias,
-    const float *__restrict__ W, const float *__restrict__ x, int n_exp, int top_k, int pre_norm, float eps, int exact,
+    const float *__restrict__ W, const float *__restrict__ x, int n_exp, int top_k, XForm xf, int exact,
     uint32_t *__restrict__ ctl, int32_t *__restrict__ ids, float *__restrict__ wts, const uint4 *__restrict__ xact,
     uint32_t *__restrict__ hact, float *__restrict__ dterm, int T) {
     constexpr int S = PER * GU_WAVES, d = 256 * PER;
@@ -173,21 +173,21 @@ __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
     // Every argument into scalar registers before the first load is issued: the compiler would
     // otherwise fetch part of them after it, a second round trip on the selection's path.
     asm volatile("" ::"s"(nib), "s"(scl), "s"(dnib), "s"(dscl), "s"(stats), "s"(bias), "s"(W), "s"(x), "s"(n_exp),
-                 "s"(top_k), "s"(pre_norm), "s"(eps), "s"(exact), "s"(ctl), "s"(ids), "s"(wts), "s"(xact), "s"(hact),
+                 "s"(top_k), "s"(xf.pre_norm), "s"(xf.eps), "s"(xf.rpost), "s"(xf.rg), "s"(xf.eg), "s"(exact), "s"(ctl), "s"(ids), "s"(wts), "s"(xact), "s"(hact),
                  "s"(dterm), "s"(T));
     const int lane = threadIdx.x & 63;
     St st;
     st.load(xact, S * 3);  // in flight during the selection
     if (blockIdx.x > 0) {
         const int b = blockIdx.x - 1, slot = b / T, t = b - slot * T;
-        select_token<PER, GU_WAVES, false>(u.sel, stats, bias, W, x, n_exp, top_k, pre_norm, eps, exact, false, false,
+        select_token<PER, GU_WAVES, false>(u.sel, stats, bias, W, x, n_exp, top_k, xf, exact, false, false,
                                            ctl, nullptr);
         const int e = __builtin_amdgcn_readfirstlane(clamp_expert(spec_id(u.sel, slot, top_k), n_exp));
         gateup_tile<PER, true>(nib, scl, dnib, dscl, e, t, T, st, act, u.terms, (uint32_t *)hprep,
                                hact + ((size_t)slot * T + t) * ACT_DW, dterm + ((size_t)slot * T + t) * d);
         return;
     }
-    select_token<PER, GU_WAVES>(u.sel, stats, bias, W, x, n_exp, top_k, pre_norm, eps, exact, true, true, ctl,
+    select_token<PER, GU_WAVES>(u.sel, stats, bias, W, x, n_exp, top_k, xf, exact, true, true, ctl,
                                 nullptr);
     if (u.sel.pass) select_weights<PER, GU_WAVES>(u.sel, n_exp, top_k);
     __syncthreads();
@@ -272,17 +272,18 @@ __global__ __launch_bounds__(256) void k_down_fold(const float *__restrict__ dte
 
 using namespace rvm;
 
-namespace {
+namespace rvm {
 
 // One decode token through the layer, scratch in ws (ws_layout(L, 1) bytes).
-int moe_decode(const rvm_layer *L, const float *x, float *out, int flags, float eps, void *ws, size_t ws_bytes) {
+int moe_decode(const rvm_layer *L, const float *x, float *out, int flags, const XForm &xf, void *ws,
+               size_t ws_bytes) {
     RVM_CHECK(layer_ok(L) && x && out && ws);
     const WsLayout lay = ws_layout(L, 1);
     RVM_CHECK(ws_bytes >= lay.total);
     uint8_t *w = (uint8_t *)ws;
     int32_t *ids = (int32_t *)(w + lay.ids);
     float *wts = (float *)(w + lay.wts);
-    int rc = launch_router(L, x, 1, flags, eps, w, lay, ids, wts, nullptr, false);
+    int rc = launch_router(L, x, 1, flags, xf, w, lay, ids, wts, nullptr, false);
     if (rc) return rc;
 
     const int Tg = 2 * L->ff / 64;
@@ -292,11 +293,11 @@ int moe_decode(const rvm_layer *L, const float *x, float *out, int flags, float 
     const size_t dn_entries = (size_t)L->n_exp * L->d * (L->ff / QK);
     const uint4 *dnib = (const uint4 *)L->down;
     const uint16_t *dscl = (const uint16_t *)((const uint8_t *)L->down + dn_entries * 16);
-    const int pre = (flags & RVM_PRE_NORM) ? 1 : 0, exact = (flags & RVM_EXACT_SELECT) ? 1 : 0;
+    const int exact = (flags & RVM_EXACT_SELECT) ? 1 : 0;
     rc = with_steps(L->d / 256, [&](auto per) {
         hipLaunchKernelGGL(k_gateup_decode<decltype(per)::value>, dim3(1 + L->top_k * Tg), dim3(GU_WAVES * 64), 0,
                            cur_stream(), gnib, gscl, dnib, dscl, (const double2 *)(w + lay.stats), L->router_bias,
-                           L->router, x, L->n_exp, L->top_k, pre, eps, exact, (uint32_t *)(w + lay.ctl), ids, wts,
+                           L->router, x, L->n_exp, L->top_k, xf, exact, (uint32_t *)(w + lay.ctl), ids, wts,
                            (const uint4 *)(w + lay.xact), (uint32_t *)(w + lay.hact), (float *)(w + lay.dterm), Tg);
         return launched();
     });
@@ -309,6 +310,9 @@ int moe_decode(const rvm_layer *L, const float *x, float *out, int flags, float 
     });
 }
 
+}  // namespace rvm
+
+namespace {
 
 // ---- The workspace-free decode (rvm_moe_decode_static) ----
 // Its scratch is this array: one copy per GPU, loaded with the library's code object and held until
@@ -342,7 +346,7 @@ int static_scratch_setup(int device) {
 
 extern "C" int rvm_moe_decode(const rvm_layer *L, const float *x, float *out, int flags, float eps, void *ws,
                               size_t ws_bytes) {
-    return moe_decode(L, x, out, flags, eps, ws, ws_bytes);
+    return moe_decode(L, x, out, flags, xform_of_flags(flags, eps), ws, ws_bytes);
 }
 
 extern "C" int rvm_moe_decode_static(const rvm_layer *L, const float *x, float *out, int flags, float eps) {
@@ -362,5 +366,5 @@ extern "C" int rvm_moe_decode_static(const rvm_layer *L, const float *x, float *
         std::lock_guard<std::mutex> lock(g_scratch_mu);
         ws = g_scratch[dev];
     }
-    return moe_decode(L, x, out, flags, eps, ws, need);
+    return moe_decode(L, x, out, flags, xform_of_flags(flags, eps), ws, need);
 }

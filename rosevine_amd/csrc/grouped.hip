@@ -21,6 +21,8 @@
 // The tile loop walks the K blocks in chunks of KC: the tile's activation rows for a chunk are
 // staged in LDS (double-buffered, one barrier per chunk), and each wave keeps the next chunk's
 // weight dwords and scales in flight while it computes the current one.
+#include <cmath>
+
 #include "internal.hpp"
 
 namespace rvm {
@@ -646,21 +648,17 @@ int launch_experts(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &la
     return launched();
 }
 
-}  // namespace rvm
-
-using namespace rvm;
-
-extern "C" int rvm_moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int flags, float eps,
-                               void *ws, size_t ws_bytes) {
+int moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int flags, const XForm &xf, void *ws,
+                size_t ws_bytes) {
     RVM_CHECK(layer_ok(L) && x && out && ws && n_tok > 0 && n_tok <= MAX_TOKENS);
-    if (n_tok == 1) return rvm_moe_decode(L, x, out, flags, eps, ws, ws_bytes);
+    if (n_tok == 1) return moe_decode(L, x, out, flags, xf, ws, ws_bytes);
     const WsLayout lay = ws_layout(L, n_tok);
     RVM_CHECK(ws_bytes >= lay.total);
     uint8_t *w = (uint8_t *)ws;
     int32_t *ids = (int32_t *)(w + lay.ids);
     float *wts = (float *)(w + lay.wts);
     int32_t *pos_of = (int32_t *)(w + lay.pos_of);
-    int rc = launch_router(L, x, n_tok, flags, eps, w, lay, ids, wts, nullptr, true);
+    int rc = launch_router(L, x, n_tok, flags, xf, w, lay, ids, wts, nullptr, true);
     if (rc) return rc;
     const int cap = tile_pairs(L, n_tok);
     if ((rc = launch_plan(ids, n_tok * L->top_k, L->n_exp, (int32_t *)(w + lay.order), pos_of,
@@ -671,4 +669,39 @@ extern "C" int rvm_moe_forward(const rvm_layer *L, const float *x, float *out, i
     hipLaunchKernelGGL(k_combine_pairs, dim3(grid_blocks(L->d / 4, 256), n_tok), dim3(256), 0, cur_stream(),
                        (const float *)(w + lay.y), pos_of, ids, wts, L->down_scale, out, L->top_k, L->d);
     return launched();
+}
+
+}  // namespace rvm
+
+using namespace rvm;
+
+extern "C" int rvm_moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int flags, float eps,
+                               void *ws, size_t ws_bytes) {
+    return moe_forward(L, x, out, n_tok, flags, xform_of_flags(flags, eps), ws, ws_bytes);
+}
+
+namespace {
+
+// The block entries' input transform: always normed, with the router's and the experts' factors.
+bool block_xform(const rvm_block_norms *nm, int flags, XForm *xf) {
+    if (!nm || !(nm->eps >= 0.0f) || !std::isfinite(nm->router_post) || (flags & ~RVM_EXACT_SELECT) != 0)
+        return false;
+    *xf = XForm{1, nm->eps, nm->router_post, nm->router_scale, nm->expert_scale};
+    return true;
+}
+
+}  // namespace
+
+extern "C" int rvm_moe_block_decode(const rvm_layer *L, const rvm_block_norms *norms, const float *o, float *out,
+                                    int flags, void *ws, size_t ws_bytes) {
+    XForm xf;
+    RVM_CHECK(block_xform(norms, flags, &xf));
+    return moe_decode(L, o, out, flags, xf, ws, ws_bytes);
+}
+
+extern "C" int rvm_moe_block_forward(const rvm_layer *L, const rvm_block_norms *norms, const float *o, float *out,
+                                     int n_tok, int flags, void *ws, size_t ws_bytes) {
+    XForm xf;
+    RVM_CHECK(block_xform(norms, flags, &xf));
+    return moe_forward(L, o, out, n_tok, flags, xf, ws, ws_bytes);
 }

@@ -317,10 +317,35 @@ int max_lds_per_block();
 // that device current (decode.hip; rvh_init calls it).
 int static_scratch_setup(int device);
 
+// How a layer input row x becomes the router's input and the experts' input. Without pre_norm
+// both are x. With it, s = 1 / sqrt(mean(x^2) + eps) (runtime/src/ops.rs:131-139) and
+//   router input  r[i] = ((x[i] * s) * rpost) * rg[i]   (runtime/src/exec.rs:493-503;
+//                                                         runtime/src/hip_exec.rs:786 with rvh_rms_norm)
+//   expert input  e[i] = (x[i] * s) * eg[i]              (exec.rs:465-468; hip_exec.rs:796)
+// each product rounded, with rg / eg absent meaning no factor (RVM_PRE_NORM alone: both x * s).
+struct XForm {
+    int pre_norm;
+    float eps;
+    float rpost;
+    const float *rg;  // [d] or null
+    const float *eg;  // [d] or null
+};
+inline XForm xform_of_flags(int flags, float eps) {
+    return XForm{(flags & RVM_PRE_NORM) ? 1 : 0, eps, 1.0f, nullptr, nullptr};
+}
+// The router and expert inputs differ (a gain or a post factor is set).
+__host__ __device__ inline bool xform_split(const XForm &xf) { return xf.rg || xf.eg || xf.rpost != 1.0f; }
+
 // Kernel launchers shared across translation units.
 // k_router (logit statistics and the Q8_0 input), then k_select unless select is false.
-int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, float eps, uint8_t *ws,
+int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, const XForm &xf, uint8_t *ws,
                   const WsLayout &lay, int32_t *ids, float *wts, float *logits, bool select);
+// One decode token (decode.hip) and n_tok tokens (grouped.hip) through the layer with input
+// transform xf; flags carries RVM_EXACT_SELECT.
+int moe_decode(const rvm_layer *L, const float *x, float *out, int flags, const XForm &xf, void *ws,
+               size_t ws_bytes);
+int moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int flags, const XForm &xf, void *ws,
+                size_t ws_bytes);
 // k_plan; with tiles set it also cuts every group into tiles of up to cap pairs: tiles[0] = count,
 // then (expert, first position in order) per tile, in expert order.
 int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart,

@@ -12,6 +12,8 @@
 // (runtime/src/exec.rs:507-517); k_plan groups (token, slot) pairs by expert (exec.rs:529-558).
 #include <math.h>
 
+#include <utility>
+
 #include "select.hpp"
 
 namespace rvm {
@@ -50,12 +52,12 @@ __device__ __forceinline__ double2 row_stats(const float4 (&wv)[F4], const float
     return make_double2(total, babs * g / (1.0 - (double)d * g) * (1.0 + 0x1p-20) + 1e-300);
 }
 
-// Q8_0 quantisation of the layer input xt (its rms_norm scale already known), one 32-block per
-// half-wave (runtime/src/ops.rs:95-105): blocks base0 + lane / 32, base0 + step + lane / 32, ...
-// to the prepared decode blocks (xact) and, when xq8 is set, the plain values in MFMA K order
-// and their scales.
+// Q8_0 quantisation of the experts' input (x, or (x * s) * eg[i] with the rms_norm scale s already
+// known), one 32-block per half-wave (runtime/src/ops.rs:95-105): blocks base0 + lane / 32,
+// base0 + step + lane / 32, ... to the prepared decode blocks (xact) and, when xq8 is set, the plain
+// values in MFMA K order and their scales.
 template <int F4>
-__device__ __forceinline__ void quant_x_blocks(const float *__restrict__ xt, int pre_norm, float scale, int base0,
+__device__ __forceinline__ void quant_x_blocks(const float *__restrict__ xt, const XForm &xf, float scale, int base0,
                                                int step, float first, uint32_t *__restrict__ xact,
                                                int8_t *__restrict__ xq8, float *__restrict__ xsc, int lane) {
     constexpr int nb = 256 * F4 / QK;
@@ -64,7 +66,8 @@ __device__ __forceinline__ void quant_x_blocks(const float *__restrict__ xt, int
         const int hb = base + (lane >> 5);
         const bool ok = hb < nb;
         float v = base == base0 ? first : (ok ? xt[hb * QK + j] : 0.0f);
-        if (pre_norm) v = v * scale;
+        if (xf.pre_norm) v = v * scale;
+        if (xf.eg) v = v * xf.eg[(ok ? hb : 0) * QK + j];
         uint16_t dbits;
         const int q = quant_q8_half(v, &dbits);
         if (xact) store_prep_half(q, dbits, j, xact + (size_t)(ok ? hb : 0) * ACT_DW, ok);
@@ -81,8 +84,7 @@ __device__ __forceinline__ void quant_x_blocks(const float *__restrict__ xt, int
 // elements [4 F4 l, 4 F4 (l + 1)) of a router row.
 template <int F4>
 __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict__ W, const float *__restrict__ x, int n_exp,
-                                                int pre_norm, float eps, double2 *__restrict__ stats,
-                                                uint32_t *__restrict__ xact) {
+                                                XForm xf, double2 *__restrict__ stats, uint32_t *__restrict__ xact) {
     constexpr int d = 256 * F4, nb = d / QK;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -91,12 +93,8 @@ __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict_
         const int base0 = ((int)blockIdx.x - groups) * RWAVES * 2 + w * 2;
         const int hb0 = base0 + (lane >> 5);
         const float first = hb0 < nb ? x[hb0 * QK + (lane & 31)] : 0.0f;
-        float scale = 1.0f;
-        if (pre_norm) {
-            float4 xv[F4];
-            scale = load_x_chunk<F4>(x, lane, pre_norm, eps, xv);
-        }
-        quant_x_blocks<F4>(x, pre_norm, scale, base0, nb, first, xact, nullptr, nullptr, lane);
+        const float scale = xf.pre_norm ? rms_scale<F4>(x, lane, xf.eps) : 1.0f;
+        quant_x_blocks<F4>(x, xf, scale, base0, nb, first, xact, nullptr, nullptr, lane);
         return;
     }
     const int e = blockIdx.x * RWAVES + w;
@@ -106,7 +104,7 @@ __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict_
 #pragma unroll
     for (int i = 0; i < F4; ++i) wv[i] = w4[i];
     float4 xv[F4];
-    load_x_chunk<F4>(x, lane, pre_norm, eps, xv);
+    load_x_chunk<F4>(x, lane, xf, xv);
     if (have) {
         const double2 st = row_stats<F4>(wv, xv, lane);
         if (lane == 0) stats[e] = st;
@@ -120,7 +118,7 @@ __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict_
 constexpr int BW = 4;
 template <int F4>
 __global__ __launch_bounds__(BW * 64) void k_router_batch(const float *__restrict__ W, const float *__restrict__ x,
-                                                          int n_tok, int n_exp, int RT, int pre_norm, float eps,
+                                                          int n_tok, int n_exp, int RT, XForm xf,
                                                           double2 *__restrict__ stats, int8_t *__restrict__ xq8,
                                                           float *__restrict__ xsc) {
     constexpr int d = 256 * F4, nb = d / QK;
@@ -150,9 +148,13 @@ __global__ __launch_bounds__(BW * 64) void k_router_batch(const float *__restric
 #pragma unroll
             for (int i = 0; i < F4; ++i) xr[i] = x4[i];
         }
-        const float scale = pre_norm ? norm_x_chunk<F4>(xt, xv, eps) : 1.0f;
+        float scale = 1.0f;
+        if (xf.pre_norm) {
+            scale = norm_x_chunk<F4>(xt, xv, xf.eps);
+            router_gain<F4>(xf, lane, xv);
+        }
         const int hb0 = base0 + (lane >> 5);
-        quant_x_blocks<F4>(xt, pre_norm, scale, base0, step, hb0 < nb ? xt[hb0 * QK + (lane & 31)] : 0.0f, nullptr,
+        quant_x_blocks<F4>(xt, xf, scale, base0, step, hb0 < nb ? xt[hb0 * QK + (lane & 31)] : 0.0f, nullptr,
                            xq8 + (size_t)t * d, xsc + (size_t)t * nb, lane);
         if (have) {
             const double2 st = row_stats<F4>(wv, xv, lane);
@@ -166,13 +168,13 @@ template <int F4>
 __global__ __launch_bounds__(SEL_WAVES * 64) void k_select(const double2 *__restrict__ stats,
                                                            const float *__restrict__ bias,
                                                            const float *__restrict__ W, const float *__restrict__ x,
-                                                           int n_exp, int top_k, int pre_norm, float eps, int exact,
+                                                           int n_exp, int top_k, XForm xf, int exact,
                                                            uint32_t *__restrict__ ctl, int32_t *__restrict__ ids,
                                                            float *__restrict__ wts, float *__restrict__ logits) {
     __shared__ SelShared<F4, SEL_WAVES> sh;
     const int tok = blockIdx.x;
     select_token<F4, SEL_WAVES>(sh, stats + (size_t)tok * n_exp, bias, W, x + (size_t)tok * 256 * F4, n_exp, top_k,
-                                pre_norm, eps, exact, true, true, ctl,
+                                xf, exact, true, true, ctl,
                                 logits ? logits + (size_t)tok * n_exp : nullptr);
     if (sh.pass) select_weights<F4, SEL_WAVES>(sh, n_exp, top_k);
     __syncthreads();
@@ -183,118 +185,223 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void k_select(const double2 *__rest
 // From FOLD_MIN_TOKENS tokens a batch holds enough (token, expert) pairs to fill the GPU with one
 // sequential fold per lane, which is cheaper than the f64 statistics and the certificate: lane l
 // of a wave is token t0 + l, the wave's expert is uniform, and each lane adds the f32 products
-// W_r[e][i] * x'[i] in element order from -0.0 (runtime/src/ops.rs:321-326), then the bias, so the
-// logits are the reference's bit for bit. The tile's 64 tokens are staged in LDS FKC columns at a
-// time (double-buffered, the next chunk's loads in flight). The wave's router row comes through
-// scalar loads, 64 floats at a time: scalar loads share the LDS wait counter and complete out of
-// order, so each batch costs one wait on everything in flight, and larger batches spill scalar
-// registers (rows as LDS broadcasts, or taken from lanes with v_readlane, measured slower). Column
-// quad q of token t sits at [q][t ^ (q & 7)], so the coalesced stores (eight quads of one token) and
-// the per-token reads (one quad of 64 tokens) are free of bank conflicts. Workgroup g also
-// quantises the Q8_0 blocks of tokens g, g + gridDim.x, ... of each staged chunk
+// W_r[e][i] * r[i] of the router input r in element order from -0.0 (runtime/src/ops.rs:321-326),
+// then the bias, so the logits are the reference's bit for bit. 512 tokens x 128 experts are 1024
+// waves, one per SIMD: each fold is a chain of d dependent adds, and the kernel is bound by that
+// chain's VALU issue (a multiply and an add per element) and by the LDS reads of the tokens.
+// The tile's 64 tokens are staged in LDS FKC columns at a time (double-buffered, the next chunk's
+// loads in flight), as the router input (the rms_norm scale and the router's factors applied once
+// per element). Column quad q of token t sits at [q][t ^ (q & 7)], so the coalesced stores (eight
+// quads of one token) and the per-token reads (one quad of 64 tokens) are free of bank conflicts.
+// The wave's router row comes through vector loads at one address for all lanes, 32 columns at a
+// time into a ring of four register sets, three sets ahead of their use: vector loads complete in
+// order, so the wait for a set never waits for the loads behind it (scalar loads would share their
+// counter with the LDS reads and complete out of order). Workgroup g also quantises the Q8_0
+// blocks of the experts' input of tokens g, g + gridDim.x, ... of each staged chunk
 // (runtime/src/ops.rs:95-105).
 constexpr int FOLD_MIN_TOKENS = RVM_FOLD_MIN_TOKENS;
 constexpr int FW = 4;     // waves (experts) per workgroup
 constexpr int FKC = 128;  // columns per staged chunk
 
-// rms_norm scale of every token (runtime/src/ops.rs:131-139), one wave per token, for the fold.
+// The inputs of the fold, one workgroup per token: the rms_norm scale s (runtime/src/ops.rs:131-139),
+// the router input ((x * s) * rpost) * rg[i] written to rin when the layer input is normed (the fold
+// reads x itself otherwise), and the Q8_0 blocks of the experts' input (x * s) * eg[i]
+// (runtime/src/ops.rs:95-105), one block per half-wave. Wave w holds blocks 2w + 8i (+1 in the upper
+// half-wave) of the row, all loaded first; the f64 sum of squares is the four waves' partial sums
+// (each a fixed tree) added in a fixed order. The reference sums sequentially; both sums lie within
+// (d - 1) 2^-53 of the exact one relative to it, so the f32 mean is the reference's unless the sum
+// sits that close to an f32 rounding boundary, when it is redone in the reference's order.
 template <int F4>
-__global__ __launch_bounds__(256) void k_norm_scales(const float *__restrict__ x, int n_tok, float eps,
-                                                     float *__restrict__ scale) {
-    const int t = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (t >= n_tok) return;
-    float4 xv[F4];
-    const float s = load_x_chunk<F4>(x + (size_t)t * 256 * F4, lane, 1, eps, xv);
-    if (lane == 0) scale[t] = s;
+__global__ __launch_bounds__(256) void k_router_prep(const float *__restrict__ x, int n_tok, XForm xf,
+                                                     float *__restrict__ rin, int8_t *__restrict__ xq8,
+                                                     float *__restrict__ xsc) {
+    constexpr int d = 256 * F4, nb = d / QK, NI = nb / 8;
+    static_assert(nb % 8 == 0, "eight blocks per round of four waves");
+    __shared__ double part[4];
+    const int t = blockIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, j = lane & 31;
+    const float *xt = x + (size_t)t * d;
+    float v[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) v[i] = xt[(2 * w + 8 * i + (lane >> 5)) * QK + j];
+    float s = 1.0f;
+    if (xf.pre_norm) {
+        double p = 0.0;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) p += (double)v[i] * (double)v[i];
+        p = wave_sum_d(p);
+        if (lane == 0) part[w] = p;
+        __syncthreads();
+        double ss = (part[0] + part[1]) + (part[2] + part[3]);
+        const double bnd = ss * (2.0 * d * 0x1p-53) * 1.01;
+        if ((float)((ss - bnd) / d) != (float)((ss + bnd) / d)) {
+            ss = 0.0;
+            for (int i = 0; i < d; ++i) {
+                const double u = (double)xt[i];
+                ss += u * u;
+            }
+        }
+        const float mean = (float)(ss / (double)d);
+        s = 1.0f / sqrtf(mean + xf.eps);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int hb = 2 * w + 8 * i + (lane >> 5), col = hb * QK + j;
+        float e = v[i];
+        if (xf.pre_norm) {
+            float r = v[i] * s;
+            e = r;
+            if (xf.rpost != 1.0f) r = r * xf.rpost;
+            if (xf.rg) r = r * xf.rg[col];
+            rin[(size_t)t * d + col] = r;
+            if (xf.eg) e = e * xf.eg[col];
+        }
+        uint16_t dbits;
+        const int q = quant_q8_half(e, &dbits);
+        xq8[(size_t)t * d + hb * QK + kperm(j)] = (int8_t)q;
+        if (j == 0) xsc[(size_t)t * nb + hb] = h2f(dbits);
+    }
+}
+
+// A raw buffer descriptor over [p, p + bytes): loads through it take an SGPR base, a 32-bit VGPR
+// offset and an immediate, and read 0 past the end.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+typedef uint32_t u32v4 __attribute__((__vector_size__(16)));
+// The whole vector is copied: a bit cast of one element of a vector type reads element 0's storage
+// with this compiler.
+__device__ __forceinline__ float4 buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const u32v4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    float4 f;
+    __builtin_memcpy(&f, &v, 16);
+    return f;
+}
+
+// Quad M of a 64-column row block: columns 4M .. 4M+3 sit in lane M of each row of 16 lanes
+// (w.x .. w.w). Each is handed to every lane by a DPP row broadcast inside the multiply
+// (v_mul_f32_dpp row_newbcast: the plain f32 product, rounded) and added to this lane's fold in
+// column order. Written out because the compiler keeps the broadcast as a separate move (its unused
+// old operand comes from another block), and as one statement per quad because the compiler puts a
+// wait state in front of every statement that holds a DPP instruction. The hardware needs two wait
+// states between a VALU write of a DPP source and its read: every w here comes from an LDS read.
+template <int M>
+__device__ __forceinline__ void fold_quad(float &acc, const float4 &w, const float4 &v) {
+    float p;
+    asm("v_mul_f32_dpp %1, %2, %6 row_newbcast:%10 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32 %0, %0, %1\n\t"
+        "v_mul_f32_dpp %1, %3, %7 row_newbcast:%10 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32 %0, %0, %1\n\t"
+        "v_mul_f32_dpp %1, %4, %8 row_newbcast:%10 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32 %0, %0, %1\n\t"
+        "v_mul_f32_dpp %1, %5, %9 row_newbcast:%10 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32 %0, %0, %1"
+        : "+v"(acc), "=&v"(p)
+        : "v"(w.x), "v"(w.y), "v"(w.z), "v"(w.w), "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w), "i"(M));
+}
+template <int BASE, int... Q>
+__device__ __forceinline__ void fold_quads(float &acc, const float4 &w, const float4 *xv,
+                                           std::integer_sequence<int, Q...>) {
+    (fold_quad<BASE + Q>(acc, w, xv[Q]), ...);  // left to right: the quads in column order
 }
 
 template <int F4>
-__global__ __launch_bounds__(FW * 64) void k_router_fold(const float *__restrict__ W, const float *__restrict__ x,
-                                                         const float *__restrict__ bias,
-                                                         const float *__restrict__ scale, int n_tok, int n_exp,
-                                                         float *__restrict__ R, int8_t *__restrict__ xq8,
-                                                         float *__restrict__ xsc) {
-    constexpr int d = 256 * F4, nb = d / QK, NCH = d / FKC, KQ = FKC / 4, LD = 64 * KQ / (FW * 64);
-    static_assert(d % FKC == 0 && FKC % QK == 0 && KQ % 4 == 0, "whole blocks per chunk");
-    __shared__ float4 xs[2][KQ][64];  // the tile's layer input, column quad q of token t at [q][t ^ (q & 7)]
-    __shared__ float sc[64];
+__global__ __launch_bounds__(FW * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_router_fold(
+    const float *__restrict__ W, const float *__restrict__ xin, const float *__restrict__ bias, int n_tok, int n_exp,
+    float *__restrict__ R) {
+    constexpr int d = 256 * F4, NCH = d / FKC, KQ = FKC / 4, LD = 64 * KQ / (FW * 64), SQ = 8, RS = KQ / SQ;
+    constexpr int WQ = d / 4, WL = (FW * WQ + FW * 64 - 1) / (FW * 64);  // row quads, and per thread
+    static_assert(FKC == 128 && NCH % 2 == 0 && RS == 4, "two 64-column row blocks and four sub-steps per chunk");
+    __shared__ float4 xs[2][KQ][64];  // the tile's router input, column quad q of token t at [q][t ^ (q & 7)]
+    __shared__ float4 wl[FW][WQ];     // the workgroup's router rows
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
-    const int t0 = blockIdx.y * 64;
-    const int ew = blockIdx.x * FW + w;
-    if (tid < 64) sc[tid] = scale ? scale[min(t0 + tid, n_tok - 1)] : 1.0f;
-    // staging: thread tid moves quad (tid % KQ) of tokens tid / KQ + j (256 / KQ), j < LD
+    // Workgroup g takes token tile g % tiles and expert group g / tiles: consecutive workgroups go to
+    // different XCDs (g % 8), so the expert groups of one tile share an XCD whenever the tile count
+    // divides 8 or is a multiple of it, and the tile's tokens are read into that XCD's L2 once.
+    const int tiles = (n_tok + 63) / 64;
+    const int t0 = (int)(blockIdx.x % tiles) * 64;
+    const int e0 = (int)(blockIdx.x / tiles) * FW;
+    const int ew = e0 + w;
+    // the rows of experts e0 .. e0 + FW - 1 (clamped), all loads issued first
+    float4 wv[WL];
+#pragma unroll
+    for (int i = 0; i < WL; ++i) {
+        const int k = min(tid + i * FW * 64, FW * WQ - 1), r = k / WQ;
+        wv[i] = ((const float4 *)(W + (size_t)min(e0 + r, n_exp - 1) * d))[k - r * WQ];
+    }
+    // staging: thread tid moves quad (tid % KQ) of tokens tid / KQ + j (256 / KQ), j < LD. Two
+    // register sets alternate: chunk c stages chunk c + 1 from its set and refills the set with
+    // chunk c + 3, so every load has two chunks' fold time to arrive.
     const int sq = tid % KQ, st = tid / KQ;
-    const float *xrow[LD];
+    const __amdgpu_buffer_rsrc_t xres = buffer_rsrc(xin, (uint32_t)((size_t)n_tok * d * 4));
+    uint32_t xoff[LD];
 #pragma unroll
-    for (int j = 0; j < LD; ++j) xrow[j] = x + (size_t)min(t0 + st + j * (256 / KQ), n_tok - 1) * d + 4 * sq;
-    // the wave's row through the constant address space: uniform loads there are scalar loads
-    typedef const __attribute__((address_space(4))) float *cfloatp;
-    const cfloatp wsrow = (cfloatp)(uintptr_t)(W + (size_t)__builtin_amdgcn_readfirstlane(min(ew, n_exp - 1)) * d);
-    float4 pf[LD];
+    for (int j = 0; j < LD; ++j) xoff[j] = (uint32_t)((min(t0 + st + j * (256 / KQ), n_tok - 1) * d + 4 * sq) * 4);
+    float4 p0[LD], pa[LD], pb[LD];
 #pragma unroll
-    for (int j = 0; j < LD; ++j) pf[j] = *(const float4 *)xrow[j];
-    __syncthreads();  // sc
-    auto stage = [&](int buf) {
+    for (int j = 0; j < LD; ++j) p0[j] = buffer_load4(xres, xoff[j], 0);
+#pragma unroll
+    for (int j = 0; j < LD; ++j) pa[j] = buffer_load4(xres, xoff[j], 1 * FKC * 4);
+#pragma unroll
+    for (int j = 0; j < LD; ++j) pb[j] = buffer_load4(xres, xoff[j], min(2, NCH - 1) * FKC * 4);
+#pragma unroll
+    for (int i = 0; i < WL; ++i) {
+        const int k = tid + i * FW * 64;
+        if (k < FW * WQ) wl[k / WQ][k % WQ] = wv[i];
+    }
+    auto stage = [&](int buf, const float4 (&p)[LD]) {
 #pragma unroll
         for (int j = 0; j < LD; ++j) {
             const int tt = st + j * (256 / KQ);
-            const float s = sc[tt];
-            const float4 v = scale ? make_float4(pf[j].x * s, pf[j].y * s, pf[j].z * s, pf[j].w * s) : pf[j];
-            xs[buf][sq][tt ^ (sq & 7)] = v;
+            xs[buf][sq][tt ^ (sq & 7)] = p[j];
         }
     };
-    stage(0);
+    stage(0, p0);
     __syncthreads();
-    // quantisation duty: tokens g, g + G, ... of the tile, 4 blocks each, one block per half-wave
-    const int G = gridDim.x, g = blockIdx.x;
-    const int njobs = (g < 64 ? (64 - g + G - 1) / G : 0) * (FKC / QK);
+    // The wave's row, 64 columns per LDS read: lane l reads columns 4 (l & 15) .. + 3 of the block,
+    // so every row of 16 lanes holds the block once and DPP row broadcasts hand each column to all
+    // lanes.
+    const float4 *wrow = wl[w] + (lane & 15);
     float acc = -0.0f;
-    for (int c = 0; c < NCH; ++c) {
+    // chunk c: set p holds chunk c + 1, staged into the other buffer halfway through the fold (that
+    // buffer was last read in chunk c - 1), then p loads chunk c + 3. Sub-step r folds quads
+    // 8r .. 8r+7 while the tokens' quads of sub-step r + 1 come from LDS; the scheduling barriers
+    // keep each sub-step's reads in their place.
+    auto chunk = [&](int c, float4 (&p)[LD]) {
         const int buf = c & 1;
-        // unconditional loads (the last chunk loads itself again, unused), so that the wait counts
-        // stay exact: a conditional load makes the compiler wait for the whole prefetch
-        const int cn = min(c + 1, NCH - 1);
+        float4 wb[2];
 #pragma unroll
-        for (int j = 0; j < LD; ++j) pf[j] = *(const float4 *)(xrow[j] + cn * FKC);
-        // the row in scalar registers, half a chunk (64 floats) at a time: one wait on the scalar
-        // loads per half, then only LDS reads are in flight and their waits are exact
-#pragma unroll 1
-        for (int h = 0; h < 2; ++h) {
-            float4 wv[KQ / 2];
+        for (int k = 0; k < 2; ++k) wb[k] = wrow[(2 * c + k) * 16];
+        float4 xv[2][SQ];
 #pragma unroll
-            for (int q = 0; q < KQ / 2; ++q) {
-                const int o = 4 * (c * KQ + h * (KQ / 2) + q);
-                wv[q] = make_float4(wsrow[o], wsrow[o + 1], wsrow[o + 2], wsrow[o + 3]);
-            }
+        for (int q = 0; q < SQ; ++q) xv[0][q] = xs[buf][q][lane ^ (q & 7)];
+        auto sub = [&](auto rc) {
+            constexpr int r = decltype(rc)::value;
+            if (r + 1 < RS)
 #pragma unroll
-            for (int q = 0; q < KQ / 2; ++q) {
-                const int qq = h * (KQ / 2) + q;
-                const float4 v = xs[buf][qq][lane ^ (qq & 7)];
-                acc = acc + wv[q].x * v.x;
-                acc = acc + wv[q].y * v.y;
-                acc = acc + wv[q].z * v.z;
-                acc = acc + wv[q].w * v.w;
-            }
-        }
-        for (int jp = 2 * w; jp < njobs; jp += 2 * FW) {
-            const int job = jp + (lane >> 5), j = lane & 31;
-            const bool ok = job < njobs;
-            const int tt = g + (ok ? job / (FKC / QK) : 0) * G, blk = job % (FKC / QK);
-            const int q = blk * (QK / 4) + (j >> 2);
-            const float4 v4 = xs[buf][q][tt ^ (q & 7)];
-            const float v = (j & 3) == 0 ? v4.x : (j & 3) == 1 ? v4.y : (j & 3) == 2 ? v4.z : v4.w;
-            uint16_t dbits;
-            const int qv = quant_q8_half(v, &dbits);
-            const int t = t0 + tt, hb = c * (FKC / QK) + blk;
-            if (ok && t < n_tok) {
-                xq8[(size_t)t * d + hb * QK + kperm(j)] = (int8_t)qv;
-                if (j == 0) xsc[(size_t)t * nb + hb] = h2f(dbits);
-            }
-        }
-        if (c + 1 < NCH) stage(buf ^ 1);
+                for (int q = 0; q < SQ; ++q) {
+                    const int qq = (r + 1) * SQ + q;
+                    xv[(r + 1) & 1][q] = xs[buf][qq][lane ^ (qq & 7)];
+                }
+            fold_quads<(r & 1) * SQ>(acc, wb[r >> 1], xv[r & 1], std::make_integer_sequence<int, SQ>{});
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        sub(std::integral_constant<int, 0>{});
+        sub(std::integral_constant<int, 1>{});
+        if (c + 1 < NCH) stage(buf ^ 1, p);
+        // unconditional loads (past the end the last chunk loads again, unused): exact wait counts
+        const int c3 = min(c + 3, NCH - 1);
+#pragma unroll
+        for (int j = 0; j < LD; ++j) p[j] = buffer_load4(xres, xoff[j], c3 * FKC * 4);
+        sub(std::integral_constant<int, 2>{});
+        sub(std::integral_constant<int, 3>{});
         __syncthreads();
+    };
+    for (int c = 0; c < NCH; c += 2) {
+        chunk(c, pa);
+        chunk(c + 1, pb);
     }
     const int t = t0 + lane;
     if (ew < n_exp && t < n_tok) R[(size_t)t * n_exp + ew] = bias ? acc + bias[ew] : acc;
@@ -421,25 +528,26 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
     }
 }
 
-int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, float eps, uint8_t *ws,
+int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, const XForm &xf, uint8_t *ws,
                   const WsLayout &lay, int32_t *ids, float *wts, float *logits, bool select) {
-    const int pre = (flags & RVM_PRE_NORM) ? 1 : 0;
+    const int pre = xf.pre_norm;
+    RVM_CHECK(pre || !xform_split(xf));  // the router's and experts' factors apply to the normed input
     return with_steps(L->d / 256, [&](auto f4) {
         constexpr int F4 = decltype(f4)::value;
         if (n_tok == 1) {  // decode: one wave per expert, and the prepared activation blocks
             const int groups = grid_blocks(L->n_exp, RWAVES), qgroups = grid_blocks(L->d / QK, 2 * RWAVES);
             hipLaunchKernelGGL(k_router<F4>, dim3(groups + qgroups), dim3(RWAVES * 64), 0, cur_stream(), L->router, x,
-                               L->n_exp, pre, eps, (double2 *)(ws + lay.stats), (uint32_t *)(ws + lay.xact));
+                               L->n_exp, xf, (double2 *)(ws + lay.stats), (uint32_t *)(ws + lay.xact));
         } else if (select && n_tok >= FOLD_MIN_TOKENS) {  // large batches: exact logits, no certificate
-            float *R = (float *)(ws + lay.stats), *sc = R + (size_t)n_tok * L->n_exp;
-            if (pre) {
-                hipLaunchKernelGGL(k_norm_scales<F4>, dim3(grid_blocks(n_tok, 4)), dim3(256), 0, cur_stream(), x,
-                                   n_tok, eps, sc);
-                if (int rc = launched()) return rc;
-            }
-            hipLaunchKernelGGL(k_router_fold<F4>, dim3(grid_blocks(L->n_exp, FW), grid_blocks(n_tok, 64)),
-                               dim3(FW * 64), 0, cur_stream(), L->router, x, L->router_bias, pre ? sc : nullptr,
-                               n_tok, L->n_exp, R, (int8_t *)(ws + lay.xq8), (float *)(ws + lay.xsc));
+            // R (the logits) in the statistics region; the normed router input in the region of the
+            // down rows y (pairs x d floats, at least n_tok x d), which the expert kernels write later
+            float *R = (float *)(ws + lay.stats), *rin = (float *)(ws + lay.y);
+            hipLaunchKernelGGL(k_router_prep<F4>, dim3(n_tok), dim3(256), 0, cur_stream(), x, n_tok, xf, rin,
+                               (int8_t *)(ws + lay.xq8), (float *)(ws + lay.xsc));
+            if (int rc = launched()) return rc;
+            hipLaunchKernelGGL(k_router_fold<F4>, dim3(grid_blocks(L->n_exp, FW) * grid_blocks(n_tok, 64)),
+                               dim3(FW * 64), 0, cur_stream(), L->router, pre ? rin : x, L->router_bias, n_tok,
+                               L->n_exp, R);
             if (int rc = launched()) return rc;
             hipLaunchKernelGGL(k_select_exact, dim3(grid_blocks(n_tok, 4)), dim3(256), 0, cur_stream(), R, n_tok,
                                L->n_exp, L->top_k, ids, wts, logits);
@@ -447,14 +555,14 @@ int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, floa
         } else {  // batches: about 16 token groups, so that the rows are read that many times
             const int rt = max(1, n_tok / 16);
             hipLaunchKernelGGL(k_router_batch<F4>, dim3(grid_blocks(L->n_exp, BW), grid_blocks(n_tok, rt)),
-                               dim3(BW * 64), 0, cur_stream(), L->router, x, n_tok, L->n_exp, rt, pre, eps,
+                               dim3(BW * 64), 0, cur_stream(), L->router, x, n_tok, L->n_exp, rt, xf,
                                (double2 *)(ws + lay.stats), (int8_t *)(ws + lay.xq8), (float *)(ws + lay.xsc));
         }
         int rc = launched();
         if (rc || !select) return rc;
         hipLaunchKernelGGL(k_select<F4>, dim3(n_tok), dim3(SEL_WAVES * 64), 0, cur_stream(),
-                           (const double2 *)(ws + lay.stats), L->router_bias, L->router, x, L->n_exp, L->top_k, pre,
-                           eps, (flags & RVM_EXACT_SELECT) ? 1 : 0, (uint32_t *)(ws + lay.ctl), ids, wts, logits);
+                           (const double2 *)(ws + lay.stats), L->router_bias, L->router, x, L->n_exp, L->top_k, xf,
+                           (flags & RVM_EXACT_SELECT) ? 1 : 0, (uint32_t *)(ws + lay.ctl), ids, wts, logits);
         return launched();
     });
 }
@@ -478,7 +586,8 @@ int rvm_router_select(const rvm_layer *layer, const float *x, int n_tok, int fla
     RVM_CHECK(layer_ok(layer) && x && n_tok > 0 && n_tok <= MAX_TOKENS && ids && weights && ws);
     const WsLayout lay = ws_layout(layer, n_tok);
     RVM_CHECK(ws_bytes >= lay.total);
-    return launch_router(layer, x, n_tok, flags, eps, (uint8_t *)ws, lay, ids, weights, logits, true);
+    return launch_router(layer, x, n_tok, flags, xform_of_flags(flags, eps), (uint8_t *)ws, lay, ids, weights, logits,
+                         true);
 }
 
 int rvm_moe_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *group_start) {

@@ -228,13 +228,45 @@ __device__ __forceinline__ float norm_x_chunk(const float *xt, float4 (&xv)[F4],
     return scale;
 }
 
-// This lane's chunk of the layer input, x or rms_norm(x): elements [4 F4 lane, 4 F4 (lane + 1)).
+// The rms_norm scale s of the row xt (every lane computes the same value).
 template <int F4>
-__device__ __forceinline__ float load_x_chunk(const float *xt, int lane, int pre_norm, float eps, float4 (&xv)[F4]) {
+__device__ __forceinline__ float rms_scale(const float *xt, int lane, float eps) {
+    float4 xv[F4];
     const float4 *x4 = (const float4 *)xt + lane * F4;
 #pragma unroll
     for (int i = 0; i < F4; ++i) xv[i] = x4[i];
-    return pre_norm ? norm_x_chunk<F4>(xt, xv, eps) : 1.0f;
+    return norm_x_chunk<F4>(xt, xv, eps);
+}
+
+// The router's factors on this lane's chunk of the normed input: ((x * s) * rpost) * rg[i].
+template <int F4>
+__device__ __forceinline__ void router_gain(const XForm &xf, int lane, float4 (&xv)[F4]) {
+    if (xf.rpost != 1.0f) {
+        const float p = xf.rpost;
+#pragma unroll
+        for (int i = 0; i < F4; ++i) xv[i] = make_float4(xv[i].x * p, xv[i].y * p, xv[i].z * p, xv[i].w * p);
+    }
+    if (xf.rg) {
+        const float4 *g4 = (const float4 *)xf.rg + lane * F4;
+#pragma unroll
+        for (int i = 0; i < F4; ++i) {
+            const float4 g = g4[i];
+            xv[i] = make_float4(xv[i].x * g.x, xv[i].y * g.y, xv[i].z * g.z, xv[i].w * g.w);
+        }
+    }
+}
+
+// This lane's chunk of the router input (elements [4 F4 lane, 4 F4 (lane + 1))): x, or the normed
+// x with the router's factors (XForm). Returns the rms_norm scale s (1 without pre_norm).
+template <int F4>
+__device__ __forceinline__ float load_x_chunk(const float *xt, int lane, const XForm &xf, float4 (&xv)[F4]) {
+    const float4 *x4 = (const float4 *)xt + lane * F4;
+#pragma unroll
+    for (int i = 0; i < F4; ++i) xv[i] = x4[i];
+    if (!xf.pre_norm) return 1.0f;
+    const float s = norm_x_chunk<F4>(xt, xv, xf.eps);
+    router_gain<F4>(xf, lane, xv);
+    return s;
 }
 
 // LDS of select_token for a workgroup of NW waves and d = 256 * F4.
@@ -266,7 +298,7 @@ struct SelShared {
 // Called by every thread.
 template <int F4, int NW>
 __device__ void exact_all(SelShared<F4, NW> &sh, const float *__restrict__ W, const float *__restrict__ bias,
-                          const float *__restrict__ xt, int n_exp, int pre_norm, float eps) {
+                          const float *__restrict__ xt, int n_exp, const XForm &xf) {
     static_assert(NW == 8, "512 threads: 128 rows x 8 column quads per pass");
     constexpr int d = 256 * F4, CH = 32, NCH = d / CH, PIT = 36, PF = 8;
     static_assert(NCH % PF == 0, "whole rounds of prefetched chunks");
@@ -275,7 +307,7 @@ __device__ void exact_all(SelShared<F4, NW> &sh, const float *__restrict__ W, co
     const int lane = tid & 63;
     if (w == 0) {
         float4 xv[F4];
-        load_x_chunk<F4>(xt, lane, pre_norm, eps, xv);
+        load_x_chunk<F4>(xt, lane, xf, xv);
 #pragma unroll
         for (int i = 0; i < F4; ++i) ((float4 *)sh.xs)[lane * F4 + i] = xv[i];
     }
@@ -339,7 +371,7 @@ __device__ void exact_all(SelShared<F4, NW> &sh, const float *__restrict__ W, co
 // a check fails; then sh.sel and sh.wsel are the exact_all path's to fill. Called by every thread.
 template <int F4, int NW>
 __device__ bool exact_candidates(SelShared<F4, NW> &sh, const float *__restrict__ W, const float *__restrict__ bias,
-                                 const float *__restrict__ xt, int n_exp, int top_k, int pre_norm, float eps) {
+                                 const float *__restrict__ xt, int n_exp, int top_k, const XForm &xf) {
     constexpr int d = 256 * F4, CM = 16, CK = 128, NCH = d / CK, PP = CK + 4, D = 6;
     static_assert(2 * CM * PP <= 128 * 36, "two product buffers fit the exact path's LDS");
     const int tid = threadIdx.x;
@@ -370,7 +402,7 @@ __device__ bool exact_candidates(SelShared<F4, NW> &sh, const float *__restrict_
         if (lane == 0) sh.ncand = ok && nc <= CM ? nc : -1;
     } else if (w == 1) {
         float4 xv[F4];
-        load_x_chunk<F4>(xt, lane, pre_norm, eps, xv);
+        load_x_chunk<F4>(xt, lane, xf, xv);
 #pragma unroll
         for (int i = 0; i < F4; ++i) ((float4 *)sh.xs)[lane * F4 + i] = xv[i];
     }
@@ -510,7 +542,8 @@ __device__ bool exact_candidates(SelShared<F4, NW> &sh, const float *__restrict_
     return sh.cok != 0;
 }
 
-// Selects top_k experts for one token. st: the token's [n_exp] statistics; xt: its layer input.
+// Selects top_k experts for one token. st: the token's [n_exp] statistics; xt: its layer input,
+// which xf turns into the router input.
 // Called by every thread of the workgroup. sh.pass tells whether the S ranking is certified; then
 // sh.sel[0..top_k) = sh.spec[0..top_k) are the reference's ids in top order and select_weights
 // computes the weights. Otherwise, with exact_here set, the exact path leaves the reference's
@@ -522,7 +555,7 @@ __device__ bool exact_candidates(SelShared<F4, NW> &sh, const float *__restrict_
 template <int F4, int NW, bool CERTIFY = true>
 __device__ void select_token(SelShared<F4, NW> &sh, const double2 *__restrict__ st, const float *__restrict__ bias,
                              const float *__restrict__ W, const float *__restrict__ xt, int n_exp, int top_k,
-                             int pre_norm, float eps, int exact, bool publish, bool exact_here,
+                             const XForm &xf, int exact, bool publish, bool exact_here,
                              uint32_t *__restrict__ ctl, float *__restrict__ lg_t) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -655,8 +688,8 @@ __device__ void select_token(SelShared<F4, NW> &sh, const double2 *__restrict__ 
         // (runtime/src/ops.rs:170-179: f64 sum in index order, expf correctly rounded) and top_k
         // by total_cmp (ops.rs:182-187) ----
         const bool done = !(publish && lg_t) &&
-                          exact_candidates<F4, NW>(sh, W, bias, xt, n_exp, top_k, pre_norm, eps);
-        if (!done) exact_all<F4, NW>(sh, W, bias, xt, n_exp, pre_norm, eps);
+                          exact_candidates<F4, NW>(sh, W, bias, xt, n_exp, top_k, xf);
+        if (!done) exact_all<F4, NW>(sh, W, bias, xt, n_exp, xf);
         if (!done && w == 0) {
             float R[4];
 #pragma unroll

@@ -54,11 +54,23 @@ class RvmLayer(C.Structure):
     ]
 
 
+class RvmBlockNorms(C.Structure):
+    """`rvm_block_norms` of include/rvmoe.h: the MoE block's router and expert input norms."""
+
+    _fields_ = [
+        ("eps", C.c_float),
+        ("router_post", C.c_float),
+        ("router_scale", C.c_void_p),
+        ("expert_scale", C.c_void_p),
+    ]
+
+
 _lib = None
 
 # name -> (restype, argtypes); every symbol of include/rvmoe.h.
 _vp, _sz, _i, _f, _u64 = C.c_void_p, C.c_size_t, C.c_int, C.c_float, C.c_uint64
 _PL = C.POINTER(RvmLayer)
+_PN = C.POINTER(RvmBlockNorms)
 SIGNATURES = {
     "rvh_init": (_i, [_i]),
     "rvh_mem_info": (_i, [C.POINTER(_sz), C.POINTER(_sz)]),
@@ -108,6 +120,8 @@ SIGNATURES = {
     "rvm_moe_plan": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "rvm_moe_decode": (_i, [_PL, _vp, _vp, _i, _f, _vp, _sz]),
     "rvm_moe_decode_static": (_i, [_PL, _vp, _vp, _i, _f]),
+    "rvm_moe_block_decode": (_i, [_PL, _PN, _vp, _vp, _i, _vp, _sz]),
+    "rvm_moe_block_forward": (_i, [_PL, _PN, _vp, _vp, _i, _i, _vp, _sz]),
     "rvm_moe_forward": (_i, [_PL, _vp, _vp, _i, _i, _f, _vp, _sz]),
 }
 

@@ -124,6 +124,44 @@ def forward(layer: MoeLayer, x: DevBuf, out: DevBuf, n_tok: int, ws: Workspace, 
                                 ws.nbytes))
 
 
+class BlockNorms:
+    """The MoE block's input norms (`rvm_block_norms`): the router input
+    ((o * s) * router_post) * router_scale and the expert input (o * s) * expert_scale, with the
+    reference's gate_inp_scale, 1/sqrt(d) and pre_ffw_norm_2 (runtime/src/hip_exec.rs:784-796)."""
+
+    def __init__(self, d: int, router_scale: np.ndarray | None, expert_scale: np.ndarray | None, eps: float = 1e-6,
+                 router_post: float | None = None):
+        if router_post is None:  # the reference's 1.0 / (n_embd as f32).sqrt(), in f32
+            router_post = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+        self.router_scale = None if router_scale is None else DevBuf.from_array(
+            np.asarray(router_scale, np.float32).reshape(d))
+        self.expert_scale = None if expert_scale is None else DevBuf.from_array(
+            np.asarray(expert_scale, np.float32).reshape(d))
+        self.struct = hip.RvmBlockNorms(eps, router_post, self.router_scale.ptr if self.router_scale else None,
+                                        self.expert_scale.ptr if self.expert_scale else None)
+
+    def ptr(self):
+        return C.byref(self.struct)
+
+
+def block_decode(layer: MoeLayer, norms: BlockNorms, o: DevBuf, out: DevBuf, ws: Workspace, flags: int = 0,
+                 o_off: int = 0, out_off: int = 0) -> None:
+    """The MoE block for one token from the hidden row o (rvm_moe_block_decode)."""
+    nb = layer.d * 4
+    check(lib().rvm_moe_block_decode(layer.ptr(), norms.ptr(), o.at(o_off, nb), out.at(out_off, nb), flags,
+                                     ws.buf.ptr, ws.nbytes))
+
+
+def block_forward(layer: MoeLayer, norms: BlockNorms, o: DevBuf, out: DevBuf, n_tok: int, ws: Workspace,
+                  flags: int = 0) -> None:
+    """The MoE block for n_tok tokens (rvm_moe_block_forward)."""
+    if n_tok > ws.n_tok:
+        raise hip.BoundsError("workspace sized for fewer tokens")
+    nb = n_tok * layer.d * 4
+    check(lib().rvm_moe_block_forward(layer.ptr(), norms.ptr(), o.at(0, nb), out.at(0, nb), n_tok, flags,
+                                      ws.buf.ptr, ws.nbytes))
+
+
 def router_select(layer: MoeLayer, x: DevBuf, n_tok: int, ws: Workspace, flags: int = 0, eps: float = 1e-6,
                   with_logits: bool = False):
     """ids[n_tok, top_k], weights[n_tok, top_k] (and logits) as host arrays."""
