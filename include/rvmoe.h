@@ -161,7 +161,12 @@ int rvm_workspace_selection(const rvm_layer *layer, int n_tok, const void *ws, i
 
 /* Router logits, softmax, top-k and renormalised weights for n_tok tokens (runtime/src/exec.rs:
  * 493-517 with the plain projection W_r . x plus bias). ids[t][j] and weights[t][j] are in the
- * reference's top order; logits (n_tok x n_exp, may be NULL) receives the f32 logits. */
+ * reference's top order; the ids are always the reference's. logits (n_tok x n_exp, may be NULL)
+ * receives the f32 logits: the reference's bits with RVM_EXACT_SELECT, from RVM_FOLD_MIN_TOKENS
+ * tokens, and for every token whose estimate-based ranking could not be certified; a certified
+ * token receives its f64 estimates rounded to f32 (within the certificate's bound of the
+ * reference's). The weights follow the same split: the reference's arithmetic on the exact paths,
+ * the estimates' (within the f32 tolerance) on certified tokens. */
 int rvm_router_select(const rvm_layer *layer, const float *x, int n_tok, int flags, float eps, int32_t *ids,
                       float *weights, float *logits, void *ws, size_t ws_bytes);
 

@@ -14,6 +14,11 @@
 // are the correctly rounded doubles of 2^(i/32) minus i << 47 (checked in that test from the
 // mathematics).
 // No HIP headers here, so that the host compiler can include it on its own.
+//
+// Notice of the restated method and its constants (Arm optimized-routines math/expf.c and
+// math/exp2f_data.c, by Szabolcs Nagy, which glibc ships as e_expf.c and e_exp2f_data.c):
+//   Copyright (c) 2017-2018, Arm Limited.
+//   SPDX-License-Identifier: MIT OR Apache-2.0 WITH LLVM-exception
 #pragma once
 #include <math.h>
 #include <stdint.h>

@@ -15,8 +15,12 @@
 //                            dot_q8_scalar does; GeGLU and the Q8_0 of h per pair finish the tile
 //   k_down_mfma           -> per (tile, 4 row tiles of 32 down rows): the same on h, into y rows
 //   k_combine_pairs       -> out[t] = sum_j (y[pos_of[t*k+j]] * scale) * weight, slot order
-// Each output is the reference's sequential fold of exact block sums, so a token's result does not
-// depend on the batch it arrives in and equals the decode path's.
+// Each pair's gate/up, h and y rows are the reference's sequential folds of exact block sums, so
+// they do not depend on the batch the pair arrives in. A token's output also carries its routing
+// weights: below RVM_FOLD_MIN_TOKENS tokens they come from the certified estimates, as in decode,
+// and the row equals the decode row bit for bit; from RVM_FOLD_MIN_TOKENS the weights are the
+// reference's arithmetic on exact logits, and the row equals the oracle's bit for bit and the
+// decode row within the f32 tolerance.
 //
 // The tile loop walks the K blocks in chunks of KC: the tile's activation rows for a chunk are
 // staged in LDS (double-buffered, one barrier per chunk), and each wave keeps the next chunk's

@@ -1,7 +1,14 @@
+// SPDX-License-Identifier: GPL-3.0-only
 // refops.hip - the reference's per-operation expert-path kernels with their rvhip.h signatures
 // (runtime/hip/rvhip.h:42-80), written for wave64: a caller of the reference ABI (its
 // runtime/src/hip_exec.rs:780-843 dispatch) can bind these symbols unchanged. The fused
 // rvm_moe_* entry points are the fast path; these keep the per-operation contract.
+//
+// Attribution: k_rms_norm, k_geglu_split, k_gather_rows and k_moe_combine follow the reference's
+// kernels of the same operators (Rowanjgc/Rosevine runtime/hip/rvhip.hip:75-90 and 401-436,
+// GPL-3.0-only) statement for statement where the bitwise contract of those operators
+// (runtime/tests/hip_ops.rs:421-439) fixes every operation; this file is therefore distributed
+// under the reference's licence. k_f32_mm and k_q4_mm are this project's own designs.
 #include "internal.hpp"
 
 namespace rvm {

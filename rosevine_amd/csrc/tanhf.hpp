@@ -7,6 +7,13 @@
 // tanhf on every f32 input (swept over all 2^32 inputs; tests/test_tanhf_restatement.py compiles
 // this header for the host and checks a sample against the host libm on every run).
 // No HIP headers here, so that the host compiler can include it on its own.
+//
+// Notice of the restated algorithm and its constants (fdlibm s_tanhf.c and s_expm1f.c, as glibc
+// ships them):
+//   Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//   Developed at SunPro, a Sun Microsystems, Inc. business.
+//   Permission to use, copy, modify, and distribute this software is freely granted, provided
+//   that this notice is preserved.
 #pragma once
 #include <math.h>
 #include <stdint.h>
