@@ -221,6 +221,35 @@ int rvm_moe_decode_static(const rvm_layer *layer, const float *x, float *out, in
 int rvm_moe_forward(const rvm_layer *layer, const float *x, float *out, int n_tok, int flags, float eps, void *ws,
                     size_t ws_bytes);
 
+/* ---- GGUF v3 expert binding (host code; the device work is rvh_upload and rvm_pack_q4) ---- */
+
+/* A parsed GGUF v3 image (runtime/src/gguf.rs:217-340): bounded, zero-copy (tensor views point
+ * into the caller's bytes, which must outlive the handle), F32 and Q4_0 tensors only. A malformed
+ * image returns hipErrorInvalidValue and rvm_gguf_last_error gives the reference's message for the
+ * fault ("bad magic", "expected GGUF version 3", "truncated header", ...). */
+typedef struct rvm_gguf rvm_gguf;
+int rvm_gguf_open(const void *data, size_t size, rvm_gguf **out);
+int rvm_gguf_close(rvm_gguf *gguf);
+/* The message of this thread's last failed rvm_gguf_* call. */
+const char *rvm_gguf_last_error(void);
+int rvm_gguf_info(const rvm_gguf *gguf, uint32_t *version, uint32_t *alignment, uint64_t *data_offset,
+                  uint64_t *n_tensors);
+/* A string metadata value (e.g. general.architecture); valid while the handle lives. */
+int rvm_gguf_meta_str(const rvm_gguf *gguf, const char *key, const char **value);
+/* A tensor by name: type (0 F32, 2 Q4_0), rank, shape in ggml order (dimension 0 contiguous;
+ * unused dimensions 1), its bytes in the image. */
+int rvm_gguf_tensor(const rvm_gguf *gguf, const char *name, uint32_t *type, uint32_t *n_dims, uint64_t shape[4],
+                    const void **data, size_t *bytes);
+/* Binds layer `layer`'s MoE tensors to the device buffers of *layer_dst (the binding of
+ * runtime/src/model.rs:33-40 at load, with the expert shapes of runtime/src/contract.rs:66-70):
+ * blk.L.ffn_gate_up_exps.weight [d, 2ff, n_exp] and blk.L.ffn_down_exps.weight [ff, d, n_exp] (Q4_0)
+ * are uploaded through staging (at least the larger tensor's bytes) and repacked into gate_up and
+ * down; blk.L.ffn_gate_inp.weight [d, n_exp] (F32) is copied into router, and
+ * blk.L.ffn_down_exps.scale [n_exp] into down_scale when that pointer is set. Shapes and types
+ * must match the layer's n_exp, d and ff. Synchronises. */
+int rvm_gguf_bind_moe(const rvm_gguf *gguf, int layer, const rvm_layer *layer_dst, void *staging,
+                      size_t staging_bytes);
+
 #ifdef __cplusplus
 }
 #endif

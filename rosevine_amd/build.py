@@ -15,7 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librvmoe.so")
-SOURCES = ["runtime.hip", "quant.hip", "router.hip", "decode.hip", "grouped.hip", "refops.hip", "attention.hip"]
+SOURCES = ["runtime.hip", "quant.hip", "router.hip", "decode.hip", "grouped.hip", "refops.hip", "attention.hip",
+           "gguf.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [

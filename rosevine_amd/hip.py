@@ -123,6 +123,14 @@ SIGNATURES = {
     "rvm_moe_block_decode": (_i, [_PL, _PN, _vp, _vp, _i, _vp, _sz]),
     "rvm_moe_block_forward": (_i, [_PL, _PN, _vp, _vp, _i, _i, _vp, _sz]),
     "rvm_moe_forward": (_i, [_PL, _vp, _vp, _i, _i, _f, _vp, _sz]),
+    "rvm_gguf_open": (_i, [_vp, _sz, C.POINTER(_vp)]),
+    "rvm_gguf_close": (_i, [_vp]),
+    "rvm_gguf_last_error": (C.c_char_p, []),
+    "rvm_gguf_info": (_i, [_vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(_u64), C.POINTER(_u64)]),
+    "rvm_gguf_meta_str": (_i, [_vp, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "rvm_gguf_tensor": (_i, [_vp, C.c_char_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(_u64),
+                             C.POINTER(_vp), C.POINTER(_sz)]),
+    "rvm_gguf_bind_moe": (_i, [_vp, _i, _PL, _vp, _sz]),
 }
 
 

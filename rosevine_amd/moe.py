@@ -25,16 +25,25 @@ FOLD_MIN_TOKENS = 256
 class MoeLayer:
     """One layer's device weights (`rvm_layer`)."""
 
-    def __init__(self, n_exp: int, top_k: int, d: int, ff: int, router: np.ndarray, bias: np.ndarray | None = None,
-                 down_scale: np.ndarray | None = None):
+    def __init__(self, n_exp: int, top_k: int, d: int, ff: int, router: np.ndarray | None,
+                 bias: np.ndarray | None = None, down_scale: np.ndarray | bool | None = None):
+        """router None leaves the router buffer to be filled later (a GGUF binding); down_scale True
+        allocates the down-scale buffer likewise."""
         self.n_exp, self.top_k, self.d, self.ff = n_exp, top_k, d, ff
-        router = np.ascontiguousarray(router, dtype=np.float32)
-        if router.shape != (n_exp, d):
-            raise ValueError(f"router must be [{n_exp}, {d}]")
-        self.router = DevBuf.from_array(router)
+        if router is None:
+            self.router = DevBuf(n_exp * d * 4)
+        else:
+            router = np.ascontiguousarray(router, dtype=np.float32)
+            if router.shape != (n_exp, d):
+                raise ValueError(f"router must be [{n_exp}, {d}]")
+            self.router = DevBuf.from_array(router)
         self.bias = None if bias is None else DevBuf.from_array(np.asarray(bias, np.float32).reshape(n_exp))
-        self.down_scale = None if down_scale is None else DevBuf.from_array(
-            np.asarray(down_scale, np.float32).reshape(n_exp))
+        if down_scale is None or down_scale is False:
+            self.down_scale = None
+        elif down_scale is True:
+            self.down_scale = DevBuf(n_exp * 4)
+        else:
+            self.down_scale = DevBuf.from_array(np.asarray(down_scale, np.float32).reshape(n_exp))
         self.gu_bytes = hip.q4_packed_bytes(n_exp, 2 * ff, d, hip.PACK_GATE_UP)
         self.dn_bytes = hip.q4_packed_bytes(n_exp, d, ff, hip.PACK_ROWS32)
         self.gate_up = DevBuf(self.gu_bytes)
