@@ -221,6 +221,36 @@ int rvm_moe_decode_static(const rvm_layer *layer, const float *x, float *out, in
 int rvm_moe_forward(const rvm_layer *layer, const float *x, float *out, int n_tok, int flags, float eps, void *ws,
                     size_t ws_bytes);
 
+/* ---- Device-call counters and the stack executor ---- */
+
+/* Device calls issued by the calling thread through this library since the last reset (the
+ * reference's per-thread Counters of runtime/src/hip.rs:167-187): kernel launches, host-to-device,
+ * device-to-host and device-to-device copies, host synchronisations (rvh_sync, rvh_event_sync, and
+ * the synchronising rvh_upload / rvh_download), and graph launches. Inside a graph capture the
+ * launches counted are the captured ones. */
+typedef struct rvm_counters {
+    uint64_t launches, h2d, d2h, d2d, syncs, graphs;
+} rvm_counters;
+int rvm_counters_get(rvm_counters *counters);
+int rvm_counters_reset(void);
+
+/* A stack of n_layers MoE layers of one shape evaluated on the device: one workspace for up to
+ * max_tokens tokens and two activation buffers, allocated here (the executor of
+ * runtime/src/hip_exec.rs:780-843 without its per-layer logits download, host selection and
+ * metadata uploads). Between layers either the synthetic stack's RMSNorm with eps (norms NULL:
+ * layer 0 takes its input as is, every later layer rms_norm of the previous output), or each
+ * layer's block norms norms[l] (the rvm_moe_block_* transform, layer 0 included). */
+typedef struct rvm_session rvm_session;
+int rvm_session_create(const rvm_layer *layers, int n_layers, const rvm_block_norms *norms, int max_tokens,
+                       float eps, rvm_session **out);
+int rvm_session_destroy(rvm_session *session);
+/* n_tok tokens (rows of x) through every layer into out: per layer only the kernels of one
+ * rvm_moe_* call (3 for one token), no transfer and no host synchronisation, so the call can be
+ * captured in one graph. flags: 0 or RVM_EXACT_SELECT. */
+int rvm_session_eval(rvm_session *session, const float *x, float *out, int n_tok, int flags);
+/* The session's workspace (for rvm_workspace_selection / rvm_workspace_fallbacks of its last layer). */
+int rvm_session_workspace(const rvm_session *session, const void **ws);
+
 /* ---- GGUF v3 expert binding (host code; the device work is rvh_upload and rvm_pack_q4) ---- */
 
 /* A parsed GGUF v3 image (runtime/src/gguf.rs:217-340): bounded, zero-copy (tensor views point

@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librvmoe.so")
 SOURCES = ["runtime.hip", "quant.hip", "router.hip", "decode.hip", "grouped.hip", "refops.hip", "attention.hip",
-           "gguf.cpp"]
+           "session.hip", "gguf.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [

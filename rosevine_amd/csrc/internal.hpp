@@ -38,7 +38,9 @@ constexpr int MIN_TILE_PAIRS = 4;  // the smallest batched tile (quad tiles of s
 
 // Library state (runtime.hip).
 hipStream_t cur_stream();
-inline int launched() { return (int)hipGetLastError(); }
+// The status of the launch just issued; every launch site calls it once, which also counts the
+// launch in this thread's device-call counters (rvm_counters_get).
+int launched();
 inline int grid_blocks(size_t n, int per) { return (int)((n + per - 1) / per); }
 
 #define RVM_CHECK(cond)                                  \

@@ -7,8 +7,15 @@
 namespace rvm {
 
 static thread_local hipStream_t g_stream = nullptr;
+// Device calls issued by this thread (the reference's per-thread Counters, runtime/src/hip.rs:167-187).
+static thread_local rvm_counters g_count{};
 
 hipStream_t cur_stream() { return g_stream; }
+
+int launched() {
+    ++g_count.launches;
+    return (int)hipGetLastError();
+}
 
 // LDS a workgroup may allocate on the current device, capped at the 64 KiB that needs no
 // per-kernel attribute.
@@ -158,22 +165,41 @@ int rvh_free(void *ptr) { return ptr ? (int)hipFree(ptr) : 0; }
 
 int rvh_upload(void *dst, const void *src, size_t bytes) {
     RVM_CHECK(dst && src);
+    ++g_count.h2d;
+    ++g_count.syncs;
     RVM_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, cur_stream()));
     return (int)hipStreamSynchronize(cur_stream());
 }
 
 int rvh_download(void *dst, const void *src, size_t bytes) {
     RVM_CHECK(dst && src);
+    ++g_count.d2h;
+    ++g_count.syncs;
     RVM_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, cur_stream()));
     return (int)hipStreamSynchronize(cur_stream());
 }
 
 int rvh_copy(void *dst, const void *src, size_t bytes) {
     RVM_CHECK(dst && src);
+    ++g_count.d2d;
     return (int)hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, cur_stream());
 }
 
-int rvh_sync(void) { return (int)hipDeviceSynchronize(); }
+int rvh_sync(void) {
+    ++g_count.syncs;
+    return (int)hipDeviceSynchronize();
+}
+
+int rvm_counters_get(rvm_counters *c) {
+    RVM_CHECK(c);
+    *c = g_count;
+    return 0;
+}
+
+int rvm_counters_reset(void) {
+    g_count = rvm_counters{};
+    return 0;
+}
 
 const char *rvh_error_string(int code) { return hipGetErrorString((hipError_t)code); }
 
@@ -194,6 +220,7 @@ int rvh_event_record(void *ev) {
 
 int rvh_event_sync(void *ev) {
     RVM_CHECK(ev);
+    ++g_count.syncs;
     return (int)hipEventSynchronize((hipEvent_t)ev);
 }
 
@@ -237,6 +264,7 @@ int rvm_graph_end(void **graph_exec) {
 
 int rvm_graph_launch(void *graph_exec) {
     RVM_CHECK(graph_exec);
+    ++g_count.graphs;
     return (int)hipGraphLaunch((hipGraphExec_t)graph_exec, cur_stream());
 }
 

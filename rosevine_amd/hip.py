@@ -123,6 +123,12 @@ SIGNATURES = {
     "rvm_moe_block_decode": (_i, [_PL, _PN, _vp, _vp, _i, _vp, _sz]),
     "rvm_moe_block_forward": (_i, [_PL, _PN, _vp, _vp, _i, _i, _vp, _sz]),
     "rvm_moe_forward": (_i, [_PL, _vp, _vp, _i, _i, _f, _vp, _sz]),
+    "rvm_counters_get": (_i, [_vp]),
+    "rvm_counters_reset": (_i, []),
+    "rvm_session_create": (_i, [_vp, _i, _vp, _i, _f, C.POINTER(_vp)]),
+    "rvm_session_destroy": (_i, [_vp]),
+    "rvm_session_eval": (_i, [_vp, _vp, _vp, _i, _i]),
+    "rvm_session_workspace": (_i, [_vp, C.POINTER(_vp)]),
     "rvm_gguf_open": (_i, [_vp, _sz, C.POINTER(_vp)]),
     "rvm_gguf_close": (_i, [_vp]),
     "rvm_gguf_last_error": (C.c_char_p, []),
@@ -148,6 +154,25 @@ def lib() -> C.CDLL:
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+class Counters(C.Structure):
+    """`rvm_counters`: device calls issued by this thread through the library."""
+
+    _fields_ = [(n, C.c_uint64) for n in ("launches", "h2d", "d2h", "d2d", "syncs", "graphs")]
+
+    def as_dict(self) -> dict:
+        return {n: getattr(self, n) for n, _ in self._fields_}
+
+
+def counters() -> dict:
+    c = Counters()
+    check(lib().rvm_counters_get(C.addressof(c)))
+    return c.as_dict()
+
+
+def reset_counters() -> None:
+    check(lib().rvm_counters_reset())
 
 
 def check(code: int) -> None:

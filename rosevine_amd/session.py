@@ -1,0 +1,62 @@
+"""A stack of MoE layers evaluated on the device (rvm_session_* of include/rvmoe.h).
+
+The executor side of the reference's MoE path (runtime/src/hip_exec.rs:780-843) with placement
+all-device and no host round trip: per layer the session issues only the kernels of one rvm_moe_*
+call, reading the previous layer's output from device memory. Between layers it applies the
+synthetic stack's RMSNorm, or each layer's block norms (the reference's router and expert norms).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import hip
+from .hip import DevBuf, RvmBlockNorms, RvmLayer, check, lib
+from .moe import BlockNorms, MoeLayer
+
+
+class Session:
+    def __init__(self, layers: list[MoeLayer], max_tokens: int, eps: float = 1e-6,
+                 norms: list[BlockNorms] | None = None):
+        if not layers:
+            raise ValueError("a session needs at least one layer")
+        if norms is not None and len(norms) != len(layers):
+            raise ValueError("one block norm set per layer")
+        self.layers, self.norms, self.max_tokens = list(layers), norms, max_tokens
+        self._larr = (RvmLayer * len(layers))(*[L.struct for L in layers])
+        self._narr = None if norms is None else (RvmBlockNorms * len(norms))(*[n.struct for n in norms])
+        h = C.c_void_p()
+        check(lib().rvm_session_create(C.addressof(self._larr), len(layers),
+                                       None if self._narr is None else C.addressof(self._narr), max_tokens, eps,
+                                       C.byref(h)))
+        self.handle = h.value
+        self.d = layers[0].d
+
+    def eval(self, x: DevBuf, out: DevBuf, n_tok: int, flags: int = 0, x_off: int = 0, out_off: int = 0) -> None:
+        """n_tok rows of x through every layer into out (rvm_session_eval)."""
+        if n_tok > self.max_tokens:
+            raise hip.BoundsError("session sized for fewer tokens")
+        nb = n_tok * self.d * 4
+        check(lib().rvm_session_eval(self.handle, x.at(x_off, nb), out.at(out_off, nb), n_tok, flags))
+
+    def selection(self, n_tok: int):
+        """ids and weights of the last layer of the last evaluation (synchronises)."""
+        ws = C.c_void_p()
+        check(lib().rvm_session_workspace(self.handle, C.byref(ws)))
+        L = self.layers[-1]
+        ids = np.empty((n_tok, L.top_k), np.int32)
+        w = np.empty((n_tok, L.top_k), np.float32)
+        check(lib().rvm_workspace_selection(L.ptr(), n_tok, ws.value, ids.ctypes.data, w.ctypes.data))
+        return ids, w
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().rvm_session_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
