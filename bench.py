@@ -35,6 +35,11 @@ ROUTER_BYTES = 128 * 2816 * 4  # 1,441,792
 # from inside this process, so the figure is the profile's, named in the line.
 MEASURED_TRAFFIC = 33_684_001
 TRAFFIC_SOURCE = "profiles/decode_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE passes)"
+# Tokens per captured graph where a token is many launches (the 30-layer workloads: 90 kernels per
+# token): graphs stay at or below 900 kernel nodes. A 4,500-node graph of the attention workload
+# ended in a host-side SIGSEGV under rocprofv3 kernel tracing, while every traced run with graphs
+# of up to 3,240 nodes completed.
+GRAPH_TOKENS = 10
 
 
 def log(msg: str) -> None:
@@ -110,10 +115,12 @@ def _timed(run, iters: int, warm: int):
 
 def measure_stack30(seed: int, n_layers: int = 30, n_tok: int = 40):
     """Single-token decode through n_layers seeded layers (router bias N(0,1), RMSNorm eps 1e-6 of
-    the previous output as the input from layer 1 on), captured in HIP graphs on the current
-    stream: (ms per token after 4 warm-up tokens, resident expert bytes). The layers' 12.9 GB of
-    experts do not fit the last-level cache, so every token reads its experts from HBM."""
-    from rosevine_amd import hip, moe, synth
+    the previous output as the input from layer 1 on) by one rvm_session, whose per-token
+    evaluations are captured in HIP graphs of GRAPH_TOKENS tokens on the current stream: (ms per
+    token after 4 warm-up tokens, resident expert bytes, device calls of one eager token). The
+    layers' 12.9 GB of experts do not fit the last-level cache, so every token reads its experts
+    from HBM."""
+    from rosevine_amd import hip, moe, session, synth
 
     E, K8, D, FF = synth.N_EXP, synth.TOP_K, synth.D, synth.FF
     layers = []
@@ -124,30 +131,36 @@ def measure_stack30(seed: int, n_layers: int = 30, n_tok: int = 40):
     hip.sync()
     stream = hip.Stream()
     stream.use()
-    ws = moe.Workspace(layers[0], 1)
+    s = session.Session(layers, max_tokens=1, eps=1e-6)
     x = hip.DevBuf.from_array(synth.tokens(seed + 300, n_tok))
-    bufs = [hip.DevBuf(D * 4) for _ in range(2)]
+    out = hip.DevBuf(D * 4)
     nb = D * 4
+    hip.sync()
+    hip.reset_counters()
+    s.eval(x, out, 1)
+    calls = hip.counters()
+    hip.sync()
 
     def capture(t0: int, n: int) -> hip.Graph:
         hip.Graph.begin()
         for t in range(t0, t0 + n):
-            moe.decode(layers[0], x, bufs[0], ws, x_off=t * nb)
-            for l in range(1, n_layers):  # the next layer's input is rms_norm(previous output, eps 1e-6)
-                moe.decode(layers[l], bufs[(l - 1) % 2], bufs[l % 2], ws, flags=hip.PRE_NORM)
+            s.eval(x, out, 1, x_off=t * nb)
         return hip.Graph.end()
 
-    warm, timed = capture(0, 4), capture(4, n_tok - 4)
+    warm = capture(0, 4)
+    timed = [capture(t, min(GRAPH_TOKENS, n_tok - t)) for t in range(4, n_tok, GRAPH_TOKENS)]
     warm.launch()
     hip.sync()
     e0, e1 = hip.Event(), hip.Event()
     e0.record()
-    timed.launch()
+    for g in timed:
+        g.launch()
     e1.record()
     e1.synchronize()
     ms = e0.elapsed_ms(e1) / (n_tok - 4)
-    warm.close()
-    timed.close()
+    for g in [warm] + timed:
+        g.close()
+    s.close()
     hip.Stream.use_default()
     stream.close()
     resident = n_layers * layers[0].weight_bytes
@@ -155,7 +168,7 @@ def measure_stack30(seed: int, n_layers: int = 30, n_tok: int = 40):
         for b in (ly.gate_up, ly.down, ly.router, ly.bias):
             if b is not None:
                 b.close()
-    return ms, resident
+    return ms, resident, calls
 
 
 def other_workload(args) -> int:
@@ -290,15 +303,17 @@ def other_workload(args) -> int:
         hip.sync()
 
         def timed(sel) -> float:
+            # reps tokens as replays of one graph of GRAPH_TOKENS tokens (at most 900 kernel nodes)
             hip.Graph.begin()
-            for _ in range(reps):
+            for _ in range(GRAPH_TOKENS):
                 one_token(sel)
             g = hip.Graph.end()
             g.launch()
             hip.sync()
             e0, e1 = hip.Event(), hip.Event()
             e0.record()
-            g.launch()
+            for _ in range(reps // GRAPH_TOKENS):
+                g.launch()
             e1.record()
             e1.synchronize()
             g.close()
@@ -335,14 +350,14 @@ def other_workload(args) -> int:
     else:  # stack30
         L = 30
         n_tok = 40
-        ms, resident = measure_stack30(args.seed, L, n_tok)
+        ms, resident, calls = measure_stack30(args.seed, L, n_tok)
         nbytes = L * (K8 * EXPERT_BYTES + ROUTER_BYTES)
         line.update({"metric": "30-layer MoE stack decode tokens/s, batch 1", "value": round(1e3 / ms, 1),
                      "unit": "tokens/s", "steps": n_tok - 4, "warmup": 4, "ms_per_step": round(ms, 6),
                      "scaling": "weak",
                      "config": {"workload": "stack30", "layers": L, "resident_bytes": resident,
                                 "routing": "per-expert bias N(0,1)", "norm": "RMSNorm eps 1e-6 between layers",
-                                "us_per_layer": round(ms * 1e3 / L, 3)},
+                                "us_per_layer": round(ms * 1e3 / L, 3), "device_calls_per_token": calls},
                      "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms / 1e3) / 1e9, 1),
                                   "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                   "frac": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -452,9 +467,10 @@ def main() -> int:
     stack = None
     if not args.no_stack:
         log("[bench] 30-layer stack (cache-cold context)")
-        s30, resident = measure_stack30(args.seed)
+        s30, resident, calls = measure_stack30(args.seed)
         stack = {"us_per_token": round(s30 * 1e3, 2), "us_per_layer": round(s30 * 1e3 / 30, 3),
-                 "layers": 30, "resident_bytes": resident,
+                 "layers": 30, "resident_bytes": resident, "executor": "rvm_session_eval",
+                 "device_calls_per_token": calls,
                  "frac_of_hbm_peak": round(30 * bytes_tok / (s30 / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
                  "note": "config 3: single-token decode through 30 layers (router bias, RMSNorm between "
                          "layers), 12.9 GB of experts, none of it held in the 256 MB last-level cache"}

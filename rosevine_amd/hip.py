@@ -11,6 +11,7 @@ raises, naming the build step.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
 
@@ -199,6 +200,19 @@ def mem_info() -> tuple[int, int]:
     return free.value, total.value
 
 
+# Set while the interpreter shuts down: finalizers then leave device memory to the process exit
+# instead of calling into a HIP runtime whose own exit handlers may already have run.
+_exiting = False
+
+
+def _at_exit() -> None:
+    global _exiting
+    _exiting = True
+
+
+atexit.register(_at_exit)
+
+
 class DevBuf:
     """An owned device allocation (hip.rs `DevBuf`)."""
 
@@ -223,6 +237,8 @@ class DevBuf:
             self.ptr = None
 
     def __del__(self):
+        if _exiting:
+            return
         try:
             self.close()
         except Exception:
@@ -268,6 +284,8 @@ class Event:
         return ms.value
 
     def __del__(self):
+        if _exiting:
+            return
         try:
             if self.ptr:
                 lib().rvh_event_destroy(self.ptr)

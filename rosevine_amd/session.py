@@ -56,6 +56,8 @@ class Session:
             self.handle = None
 
     def __del__(self):
+        if hip._exiting:
+            return
         try:
             self.close()
         except Exception:
