@@ -234,6 +234,14 @@ typedef struct rvm_counters {
 int rvm_counters_get(rvm_counters *counters);
 int rvm_counters_reset(void);
 
+/* Diagnostic builds only (compiled with RVM_PHASE_TRACE; other builds return hipErrorNotSupported):
+ * copies the realtime-counter stamps (100 MHz, u64) of the last decode call to host memory of at
+ * least 3 x 4096 x 8 x 8 bytes: [kernel][workgroup][point] for k_router (0: entry, 1: done),
+ * k_gateup_decode (0: entry, 1: expert known, 2: first block terms formed, 3: h block ready, 4:
+ * down terms stored) and k_down_fold (0: entry, 1: rows folded, 2: output stored). No counterpart
+ * in the reference: it measures where a decode token's time goes across workgroups and XCDs. */
+int rvm_phase_trace(void *host, size_t bytes);
+
 /* A stack of n_layers MoE layers of one shape evaluated on the device: one workspace for up to
  * max_tokens tokens and two activation buffers, allocated here (the executor of
  * runtime/src/hip_exec.rs:780-843 without its per-layer logits download, host selection and

@@ -22,6 +22,15 @@
 namespace rvm {
 
 constexpr int GU_WAVES = 8;  // K split of the gate_up tile
+
+#ifdef RVM_PHASE_TRACE
+// k_gateup_decode (0): 0 entry, 1 expert known (workgroup 0: ranking done), 2 wave 0's block terms
+// formed (workgroup 0: ids and weights published), 3 h block ready, 4 down terms stored;
+// k_down_fold (1): 0 entry, 1 slot rows folded, 2 output stored
+namespace {
+__device__ unsigned long long g_stamp[2 * TRACE_WG * TRACE_PT];
+}  // namespace
+#endif
 constexpr int MAX_TOPK = 8;
 
 // Staging of n uint4 from global to LDS in two steps, so that a kernel can issue these loads
@@ -117,6 +126,7 @@ __device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const
     __builtin_amdgcn_sched_barrier(0);
     float tv[PER];
     lane_terms<PER>(wv, sv, act + w * PER * 3, tv);
+    RVM_STAMP(g_stamp, 0, 2);
 #pragma unroll
     for (int i = 0; i < PER; ++i) terms[w * PER + i][lane] = tv[i];
     __syncthreads();
@@ -135,6 +145,7 @@ __device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const
         store_prep_half(q, dbits, lane & 31, hprep, lane < 32);
     }
     __syncthreads();
+    RVM_STAMP(g_stamp, 0, 3);
     {
         const uint4 *hp = (const uint4 *)hprep;
         const uint4 a0 = hp[0], a1 = hp[1];
@@ -147,6 +158,7 @@ __device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const
             if (r < d) dterm[r] = term;
         }
     }
+    RVM_STAMP(g_stamp, 0, 4);
 }
 
 __device__ __forceinline__ int clamp_expert(int e, int n_exp) { return (unsigned)e < (unsigned)n_exp ? e : 0; }
@@ -176,6 +188,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
                  "s"(top_k), "s"(xf.pre_norm), "s"(xf.eps), "s"(xf.rpost), "s"(xf.rg), "s"(xf.eg), "s"(exact), "s"(ctl), "s"(ids), "s"(wts), "s"(xact), "s"(hact),
                  "s"(dterm), "s"(T));
     const int lane = threadIdx.x & 63;
+    RVM_STAMP(g_stamp, 0, 0);
     St st;
     st.load(xact, S * 3);  // in flight during the selection
     if (blockIdx.x > 0) {
@@ -183,12 +196,14 @@ __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
         select_token<PER, GU_WAVES, false>(u.sel, stats, bias, W, x, n_exp, top_k, xf, exact, false, false,
                                            ctl, nullptr);
         const int e = __builtin_amdgcn_readfirstlane(clamp_expert(spec_id(u.sel, slot, top_k), n_exp));
+        RVM_STAMP(g_stamp, 0, 1);
         gateup_tile<PER, true>(nib, scl, dnib, dscl, e, t, T, st, act, u.terms, (uint32_t *)hprep,
                                hact + ((size_t)slot * T + t) * ACT_DW, dterm + ((size_t)slot * T + t) * d);
         return;
     }
     select_token<PER, GU_WAVES>(u.sel, stats, bias, W, x, n_exp, top_k, xf, exact, true, true, ctl,
                                 nullptr);
+    RVM_STAMP(g_stamp, 0, 1);
     if (u.sel.pass) select_weights<PER, GU_WAVES>(u.sel, n_exp, top_k);
     __syncthreads();
     if (threadIdx.x < 64) {
@@ -208,6 +223,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
         if (lane == 0) n_fix = __popcll(nm);
     }
     __syncthreads();
+    RVM_STAMP(g_stamp, 0, 2);
     // experts the S ranking missed: all their tiles, into the correction rows (rare: the exact
     // selection changed the set of experts)
     for (int m = 0; m < n_fix; ++m)
@@ -239,6 +255,7 @@ __global__ __launch_bounds__(256) void k_down_fold(const float *__restrict__ dte
     const int row = blockIdx.x * 32 + (threadIdx.x & 31);
     const int k = threadIdx.x >> 5;  // slot
     const int kc = min(k, top_k - 1);
+    RVM_STAMP(g_stamp, 1, 0);
     float v[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) v[t] = dterm[((size_t)kc * T + t) * d + row];
@@ -257,6 +274,7 @@ __global__ __launch_bounds__(256) void k_down_fold(const float *__restrict__ dte
 #pragma unroll
     for (int t = 0; t < T; ++t) acc = acc + v[t];
     if (k < top_k) ys[k][threadIdx.x & 31] = acc;
+    RVM_STAMP(g_stamp, 1, 1);
     __syncthreads();
     if (threadIdx.x < 32) {
         float o = 0.0f;
@@ -266,6 +284,7 @@ __global__ __launch_bounds__(256) void k_down_fold(const float *__restrict__ dte
         }
         out[row] = o;
     }
+    RVM_STAMP(g_stamp, 1, 2);
 }
 
 }  // namespace rvm
@@ -328,6 +347,15 @@ void *g_scratch[MAX_DEVICES];
 }  // namespace
 
 namespace rvm {
+
+int phase_trace_decode(void *host) {
+#ifdef RVM_PHASE_TRACE
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_stamp), sizeof(g_stamp));
+#else
+    (void)host;
+    return (int)hipErrorNotSupported;
+#endif
+}
 
 // Takes the scratch array's address on `device`, which must be current; idempotent.
 int static_scratch_setup(int device) {

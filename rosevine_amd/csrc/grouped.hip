@@ -87,9 +87,10 @@ struct TileLds {
 // The block sums of one tile: rows of the wave's row tile (entry groups tb .. tb+S-1, NR pieces of
 // 16 plane lanes; block b uses group b mod S at lane offset 32 (b / S)) against the tile's R
 // activation rows (K = width, nb = width / 32 blocks). acc[mt][r][i] is the output of pair
-// 16 mt + 4 g + i and plane lane 16 r + m, for lane = 16 g + m. All waves take part in the staging
-// and barriers; waves without a row tile (active false) skip the weights and MFMAs.
-template <int MT, int NR, int KC>
+// 16 mt + 4 g + i and plane lane 16 r + m, for lane = 16 g + m. Only the first LIVE m-tiles are
+// computed (the others hold no pair; their acc stays 0). All waves take part in the staging and
+// barriers; waves without a row tile (active false) skip the weights and MFMAs.
+template <int MT, int NR, int KC, int LIVE>
 __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const uint16_t *__restrict__ scl,
                                           size_t tb, int S, bool active, const int8_t *__restrict__ src,
                                           const float *__restrict__ ssrc, int width, TileLds<MT, NR, KC> &sh,
@@ -216,7 +217,7 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
             long a[MT];
             float4 dx[MT];
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
+            for (int mt = 0; mt < LIVE; ++mt) {
                 a[mt] = *(const long *)(sh.xs[buf] + (mt * 16 + m) * XP + kb * QK + g * 8);
                 dx[mt] = *(const float4 *)(sh.ss[buf] + kb * R + mt * 16 + 4 * g);
             }
@@ -226,13 +227,13 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
             for (int r = 0; r < NR; ++r) {
                 const long bw = weights16(wn[kb][r]);
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
+                for (int mt = 0; mt < LIVE; ++mt)
                     sm[mt][r] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[mt], bw, v4i{0, 0, 0, 0}, 0, 0, 0);
             }
 #pragma unroll
             for (int r = 0; r < NR; ++r)
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) fold_block(acc[mt][r], sm[mt][r], dw[r], dx[mt]);
+                for (int mt = 0; mt < LIVE; ++mt) fold_block(acc[mt][r], sm[mt][r], dw[r], dx[mt]);
         }
         wave_lds_sync();  // the next chunk's scale stores stay behind these reads
     };
@@ -294,7 +295,9 @@ __global__ __launch_bounds__(MW * 64) void k_gateup_mfma(const uint8_t *__restri
     const int rt = blockIdx.x * MW + (threadIdx.x >> 6);
     const bool active = rt < Tg;
     float acc[MT][4][4];
-    tile_sums<MT, 4, KC>(nib, scl, ((size_t)e * Tg + (active ? rt : 0)) * nb, nb, active, xq8, xsc, d, sh, acc);
+    // every m-tile, also an empty one: a second instance of the loop for tiles of at most 16 pairs
+    // measured slower here (the down kernel keeps one)
+    tile_sums<MT, 4, KC, MT>(nib, scl, ((size_t)e * Tg + (active ? rt : 0)) * nb, nb, active, xq8, xsc, d, sh, acc);
     if (!active) return;
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -342,7 +345,12 @@ __global__ __launch_bounds__(MW * 64) void k_down_mfma(const uint8_t *__restrict
     const int rt = blockIdx.x * MW + (threadIdx.x >> 6);
     const bool active = rt < Td;
     float acc[MT][2][4];
-    tile_sums<MT, 2, KC>(nib, scl, ((size_t)e * Td + (active ? rt : 0)) * Sd, Sd, active, hq8, hsc, ff, sh, acc);
+    // a tile of at most 16 pairs runs the loop of one m-tile
+    const size_t tb = ((size_t)e * Td + (active ? rt : 0)) * Sd;
+    if (MT > 1 && cnt <= 16)
+        tile_sums<MT, 2, KC, 1>(nib, scl, tb, Sd, active, hq8, hsc, ff, sh, acc);
+    else
+        tile_sums<MT, 2, KC, MT>(nib, scl, tb, Sd, active, hq8, hsc, ff, sh, acc);
     if (!active) return;
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
 #pragma unroll

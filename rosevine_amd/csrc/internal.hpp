@@ -353,4 +353,23 @@ int moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int f
 int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart,
                 int32_t *tiles, int cap);
 
+// Phase stamps of the decode kernels, in diagnostic builds only (-DRVM_PHASE_TRACE; other builds
+// compile RVM_STAMP to nothing): thread 0 of each workgroup stores the 100 MHz realtime counter at
+// point s of kernel k into its translation unit's array [k][workgroup][point] with a vector store,
+// so that one decode call's phases can be read back across workgroups and XCDs.
+constexpr int TRACE_WG = 4096, TRACE_PT = 8;
+#ifdef RVM_PHASE_TRACE
+#define RVM_STAMP(arr, k, s)                                                                              \
+    do {                                                                                                  \
+        if (threadIdx.x == 0 && blockIdx.x < (unsigned)rvm::TRACE_WG)                                     \
+            (arr)[((k) * rvm::TRACE_WG + blockIdx.x) * rvm::TRACE_PT + (s)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define RVM_STAMP(arr, k, s) ((void)0)
+#endif
+// Copy the stamps of k_router ([1][TRACE_WG][TRACE_PT]) and of k_gateup_decode, k_down_fold
+// ([2][TRACE_WG][TRACE_PT]) to host memory; hipErrorNotSupported in other builds.
+int phase_trace_router(void *host);
+int phase_trace_decode(void *host);
+
 }  // namespace rvm

@@ -18,6 +18,12 @@
 
 namespace rvm {
 
+#ifdef RVM_PHASE_TRACE
+namespace {
+__device__ unsigned long long g_stamp[TRACE_WG * TRACE_PT];  // k_router: 0 entry, 1 done
+}  // namespace
+#endif
+
 constexpr int RWAVES = 1;  // waves (experts) per router workgroup: one expert per CU spreads the row loads
 constexpr int SEL_WAVES = 8;  // waves of the selecting workgroup
 
@@ -89,12 +95,14 @@ __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict_
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int groups = (n_exp + RWAVES - 1) / RWAVES;
+    RVM_STAMP(g_stamp, 0, 0);
     if ((int)blockIdx.x >= groups) {
         const int base0 = ((int)blockIdx.x - groups) * RWAVES * 2 + w * 2;
         const int hb0 = base0 + (lane >> 5);
         const float first = hb0 < nb ? x[hb0 * QK + (lane & 31)] : 0.0f;
         const float scale = xf.pre_norm ? rms_scale<F4>(x, lane, xf.eps) : 1.0f;
         quant_x_blocks<F4>(x, xf, scale, base0, nb, first, xact, nullptr, nullptr, lane);
+        RVM_STAMP(g_stamp, 0, 1);
         return;
     }
     const int e = blockIdx.x * RWAVES + w;
@@ -109,6 +117,7 @@ __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict_
         const double2 st = row_stats<F4>(wv, xv, lane);
         if (lane == 0) stats[e] = st;
     }
+    RVM_STAMP(g_stamp, 0, 1);
 }
 
 // Batched statistics: workgroup (g, r) keeps the rows of experts BW g .. BW g + BW-1 in registers
@@ -573,6 +582,15 @@ int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int3
     hipLaunchKernelGGL(k_plan, dim3(1), dim3(1024), 0, cur_stream(), ids, n_pairs, n_exp, order, pos_of, gstart,
                        tiles, cap);
     return launched();
+}
+
+int phase_trace_router(void *host) {
+#ifdef RVM_PHASE_TRACE
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_stamp), sizeof(g_stamp));
+#else
+    (void)host;
+    return (int)hipErrorNotSupported;
+#endif
 }
 
 }  // namespace rvm

@@ -201,6 +201,13 @@ int rvm_counters_reset(void) {
     return 0;
 }
 
+int rvm_phase_trace(void *host, size_t bytes) {
+    constexpr size_t per = (size_t)TRACE_WG * TRACE_PT * sizeof(uint64_t);
+    RVM_CHECK(host && bytes >= 3 * per);
+    if (int rc = phase_trace_router(host)) return rc;
+    return phase_trace_decode((uint8_t *)host + per);
+}
+
 const char *rvh_error_string(int code) { return hipGetErrorString((hipError_t)code); }
 
 int rvh_event_create(void **out) {

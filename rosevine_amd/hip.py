@@ -126,6 +126,7 @@ SIGNATURES = {
     "rvm_moe_forward": (_i, [_PL, _vp, _vp, _i, _i, _f, _vp, _sz]),
     "rvm_counters_get": (_i, [_vp]),
     "rvm_counters_reset": (_i, []),
+    "rvm_phase_trace": (_i, [_vp, _sz]),
     "rvm_session_create": (_i, [_vp, _i, _vp, _i, _f, C.POINTER(_vp)]),
     "rvm_session_destroy": (_i, [_vp]),
     "rvm_session_eval": (_i, [_vp, _vp, _vp, _i, _i]),

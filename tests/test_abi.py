@@ -81,3 +81,12 @@ def test_bounds_are_checked_before_any_call(rvlib):
         pass
     else:
         raise AssertionError("out-of-allocation range accepted")
+
+
+def test_phase_trace_only_in_the_diagnostic_build(rvlib):
+    """The normal build compiles the decode kernels' phase stamps out: rvm_phase_trace refuses a
+    short buffer and otherwise reports hipErrorNotSupported, with no device call."""
+    buf = np.zeros(3 * 4096 * 8, np.uint64)
+    assert rvlib.rvm_phase_trace(buf.ctypes.data, buf.nbytes - 8) != 0
+    assert rvlib.rvm_phase_trace(buf.ctypes.data, buf.nbytes) == 801  # hipErrorNotSupported
+    assert not buf.any()
