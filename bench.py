@@ -33,7 +33,7 @@ ROUTER_BYTES = 128 * 2816 * 4  # 1,441,792
 # HBM bytes one decode call moves (read + written): rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
 # this workload, each calibrated against a device copy of known size. The counters cannot be read
 # from inside this process, so the figure is the profile's, named in the line.
-MEASURED_TRAFFIC = 33_684_001
+MEASURED_TRAFFIC = 33_700_443
 TRAFFIC_SOURCE = "profiles/decode_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE passes)"
 # Tokens per captured graph where a token is many launches (the 30-layer workloads: 90 kernels per
 # token): graphs stay at or below 900 kernel nodes. A 4,500-node graph of the attention workload
