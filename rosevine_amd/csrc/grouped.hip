@@ -4,7 +4,8 @@
 //
 //   router (router.hip)   -> ids, weights, Q8_0 activation rows per token (K order of kperm)
 //   k_plan (router.hip)   -> pairs stably grouped by expert, each group cut into tiles of up to
-//                            32 pairs (batches of 8+ pairs per expert on average) or 4 (smaller)
+//                            32 pairs for gate/up and 48 for down (batches of 8+ pairs per expert
+//                            on average), or 4 (smaller)
 //   k_gateup_quad,        -> 4-pair tiles: one wave per (tile, 64 weight rows); the 16-block
 //   k_down_quad              v_mfma_i32_4x4x4_16b_i8 gives each lane its row's exact block sums
 //                            for the 4 pairs, so the f32 fold spends nothing on empty pair places
@@ -13,7 +14,8 @@
 //                            each block's exact int32 sum for 16 pairs x 16 rows; the f32 terms
 //                            (sumi as f32) * (d_w * d_x) are folded in block order per output, as
 //                            dot_q8_scalar does; GeGLU and the Q8_0 of h per pair finish the tile
-//   k_down_mfma           -> per (tile, 4 row tiles of 32 down rows): the same on h, into y rows
+//   k_down_mfma           -> per (48-pair tile, 4 row tiles of 32 down rows): the same on h, into
+//                            y rows
 //   k_combine_pairs       -> out[t] = sum_j (y[pos_of[t*k+j]] * scale) * weight, slot order
 // Each pair's gate/up, h and y rows are the reference's sequential folds of exact block sums, so
 // they do not depend on the batch the pair arrives in. A token's output also carries its routing
@@ -345,10 +347,12 @@ __global__ __launch_bounds__(MW * 64) void k_down_mfma(const uint8_t *__restrict
     const int rt = blockIdx.x * MW + (threadIdx.x >> 6);
     const bool active = rt < Td;
     float acc[MT][2][4];
-    // a tile of at most 16 pairs runs the loop of one m-tile
+    // a tile runs the loop of its occupied m-tiles only
     const size_t tb = ((size_t)e * Td + (active ? rt : 0)) * Sd;
     if (MT > 1 && cnt <= 16)
         tile_sums<MT, 2, KC, 1>(nib, scl, tb, Sd, active, hq8, hsc, ff, sh, acc);
+    else if (MT > 2 && cnt <= 32)
+        tile_sums<MT, 2, KC, (MT > 2 ? 2 : MT)>(nib, scl, tb, Sd, active, hq8, hsc, ff, sh, acc);
     else
         tile_sums<MT, 2, KC, MT>(nib, scl, tb, Sd, active, hq8, hsc, ff, sh, acc);
     if (!active) return;
@@ -630,18 +634,23 @@ int launch_experts_quad(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayou
 }
 
 // Pairs per tile: quads while the groups are small (fewer pairs than 8 per expert on average),
-// else 32 (two 16-pair m-tiles), so that a typical group fits one tile and its weights are
-// streamed once.
+// else the MFMA tiles (32 pairs for gate/up, 48 for down), so that a typical group fits one tile
+// and its weights are streamed once.
 inline int tile_pairs(const rvm_layer *L, int n_tok) {
     const long pairs = (long)n_tok * L->top_k;
     return pairs >= 8L * L->n_exp ? 32 : QUAD;
 }
 
-template <int MT>
+// The 16x16 MFMA kernels: gate/up on tiles of 16 MT pairs (lay.tiles), down on tiles of 16 MD pairs
+// (lay.tiles2). Gate/up keeps two m-tiles: with three its registers allow two waves per SIMD instead
+// of three (200 against 186 us for 512 tokens); down runs three at three waves per SIMD (73 against
+// 82.5 us), each of its tiles through the loop of only its occupied m-tiles.
+template <int MT, int MD>
 int launch_experts(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &lay) {
     const int32_t *tiles = (const int32_t *)(w + lay.tiles);
+    const int32_t *tiles2 = (const int32_t *)(w + lay.tiles2);
     const int32_t *gstart = (const int32_t *)(w + lay.gstart);
-    const int nt = (int)max_tiles(L, n_tok, 16 * MT);
+    const int nt = (int)max_tiles(L, n_tok, 16 * MT), nd = (int)max_tiles(L, n_tok, 16 * MD);
     const size_t gu_entries = (size_t)L->n_exp * 2 * L->ff * (L->d / QK);
     const uint8_t *gnib = (const uint8_t *)L->gate_up;
     const uint16_t *gscl = (const uint16_t *)(gnib + gu_entries * 16);
@@ -654,8 +663,8 @@ int launch_experts(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &la
     const size_t dn_entries = (size_t)L->n_exp * L->d * (L->ff / QK);
     const uint8_t *dnib = (const uint8_t *)L->down;
     const uint16_t *dscl = (const uint16_t *)(dnib + dn_entries * 16);
-    hipLaunchKernelGGL(k_down_mfma<MT>, dim3(grid_blocks(L->d / 32, MW), nt), dim3(MW * 64), 0, cur_stream(), dnib,
-                       dscl, tiles, gstart, (const int8_t *)(w + lay.hq8), (const float *)(w + lay.hsc),
+    hipLaunchKernelGGL(k_down_mfma<MD>, dim3(grid_blocks(L->d / 32, MW), nd), dim3(MW * 64), 0, cur_stream(), dnib,
+                       dscl, tiles2, gstart, (const int8_t *)(w + lay.hq8), (const float *)(w + lay.hsc),
                        (float *)(w + lay.y), L->d, L->ff);
     return launched();
 }
@@ -672,11 +681,14 @@ int moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int f
     int32_t *pos_of = (int32_t *)(w + lay.pos_of);
     int rc = launch_router(L, x, n_tok, flags, xf, w, lay, ids, wts, nullptr, true);
     if (rc) return rc;
+    constexpr int GU_MT = 2, DN_MT = 3;  // m-tiles per tile of the two MFMA kernels
     const int cap = tile_pairs(L, n_tok);
+    const bool quad = cap == QUAD;
     if ((rc = launch_plan(ids, n_tok * L->top_k, L->n_exp, (int32_t *)(w + lay.order), pos_of,
-                          (int32_t *)(w + lay.gstart), (int32_t *)(w + lay.tiles), cap)))
+                          (int32_t *)(w + lay.gstart), (int32_t *)(w + lay.tiles), quad ? QUAD : 16 * GU_MT,
+                          quad ? nullptr : (int32_t *)(w + lay.tiles2), 16 * DN_MT)))
         return rc;
-    rc = cap == QUAD ? launch_experts_quad(L, n_tok, w, lay) : launch_experts<2>(L, n_tok, w, lay);
+    rc = quad ? launch_experts_quad(L, n_tok, w, lay) : launch_experts<GU_MT, DN_MT>(L, n_tok, w, lay);
     if (rc) return rc;
     hipLaunchKernelGGL(k_combine_pairs, dim3(grid_blocks(L->d / 4, 256), n_tok), dim3(256), 0, cur_stream(),
                        (const float *)(w + lay.y), pos_of, ids, wts, L->down_scale, out, L->top_k, L->d);

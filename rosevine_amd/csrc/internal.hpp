@@ -244,6 +244,7 @@ struct WsLayout {
     size_t hq8;     // i8[pairs][ff]: plain Q8_0 values of h, in plan order (batched path)
     size_t hsc;     // f32[pairs][ff/32]
     size_t tiles;   // i32[1 + 2 max_tiles]: the plan's tiles (4 or 32 pairs)
+    size_t tiles2;  // the same for the down kernel of the 16-pair MFMA path (48-pair tiles)
     size_t total;
 };
 
@@ -282,6 +283,7 @@ inline WsLayout ws_layout(const rvm_layer *L, int n_tok) {
     w.hq8 = take(pairs * L->ff);
     w.hsc = take(pairs * (L->ff / QK) * 4);
     w.tiles = take((1 + 2 * max_tiles(L, n_tok, MIN_TILE_PAIRS)) * 4);
+    w.tiles2 = take((1 + 2 * max_tiles(L, n_tok, MIN_TILE_PAIRS)) * 4);
     w.total = o;
     return w;
 }
@@ -349,9 +351,9 @@ int moe_decode(const rvm_layer *L, const float *x, float *out, int flags, const 
 int moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int flags, const XForm &xf, void *ws,
                 size_t ws_bytes);
 // k_plan; with tiles set it also cuts every group into tiles of up to cap pairs: tiles[0] = count,
-// then (expert, first position in order) per tile, in expert order.
+// then (expert, first position in order) per tile, in expert order; tiles2 likewise with cap2.
 int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart,
-                int32_t *tiles, int cap);
+                int32_t *tiles, int cap, int32_t *tiles2 = nullptr, int cap2 = 0);
 
 // Phase stamps of the decode kernels, in diagnostic builds only (-DRVM_PHASE_TRACE; other builds
 // compile RVM_STAMP to nothing): thread 0 of each workgroup stores the 100 MHz realtime counter at

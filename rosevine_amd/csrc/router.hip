@@ -442,10 +442,12 @@ __global__ __launch_bounds__(256) void k_select_exact(const float *__restrict__ 
 // Stable counting sort of pair ids by expert in one workgroup of 16 waves: wave w owns a
 // contiguous chunk of pairs; per-(wave, expert) counts are scanned in (expert, wave) order, then
 // each wave places its pairs 64 at a time, ranking equal experts among lower lanes with ballots.
-// Ids outside [0, n_exp) are neither counted nor placed (pos_of = -1).
+// Ids outside [0, n_exp) are neither counted nor placed (pos_of = -1). With tiles (and tiles2)
+// set, every group is also cut into tiles of up to cap (cap2) pairs.
 __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, int n, int n_exp,
                                                int32_t *__restrict__ order, int32_t *__restrict__ pos_of,
-                                               int32_t *__restrict__ gstart, int32_t *__restrict__ tiles, int cap) {
+                                               int32_t *__restrict__ gstart, int32_t *__restrict__ tiles, int cap,
+                                               int32_t *__restrict__ tiles2, int cap2) {
     __shared__ int cnt[16][256];
     __shared__ int tot[257];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -465,25 +467,29 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
     }
     __syncthreads();
     if (w == 0) {  // exclusive scans of the group sizes and of their tile counts, 4 experts a lane
-        int c[4], t[4], cs = 0, ts = 0;
+        const int cp2 = tiles2 ? cap2 : 1;
+        int c[4], t[4], t2[4], cs = 0, ts = 0, ts2 = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int e = 4 * lane + k;
             c[k] = e < n_exp ? tot[e] : 0;
             t[k] = (c[k] + cap - 1) / cap;
+            t2[k] = (c[k] + cp2 - 1) / cp2;
             cs += c[k];
             ts += t[k];
+            ts2 += t2[k];
         }
-        int ic = cs, it = ts;
+        int ic = cs, it = ts, it2 = ts2;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            const int nc = __shfl_up(ic, o), nt = __shfl_up(it, o);
+            const int nc = __shfl_up(ic, o), nt = __shfl_up(it, o), nt2 = __shfl_up(it2, o);
             if (lane >= o) {
                 ic += nc;
                 it += nt;
+                it2 += nt2;
             }
         }
-        int run = ic - cs, nt = it - ts;
+        int run = ic - cs, nt = it - ts, nt2 = it2 - ts2;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int e = 4 * lane + k;
@@ -494,13 +500,20 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
                         tiles[1 + 2 * (nt + q)] = e;
                         tiles[2 + 2 * (nt + q)] = run + q * cap;
                     }
+                if (tiles2)
+                    for (int q = 0; q < t2[k]; ++q) {
+                        tiles2[1 + 2 * (nt2 + q)] = e;
+                        tiles2[2 + 2 * (nt2 + q)] = run + q * cap2;
+                    }
             }
             run += c[k];
             nt += t[k];
+            nt2 += t2[k];
         }
         if (lane == 63) {
             tot[n_exp] = ic;
             if (tiles) tiles[0] = it;
+            if (tiles2) tiles2[0] = it2;
         }
     }
     __syncthreads();
@@ -577,10 +590,10 @@ int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, cons
 }
 
 int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart,
-                int32_t *tiles, int cap) {
-    RVM_CHECK(cap >= 1);
+                int32_t *tiles, int cap, int32_t *tiles2, int cap2) {
+    RVM_CHECK(cap >= 1 && (!tiles2 || cap2 >= 1));
     hipLaunchKernelGGL(k_plan, dim3(1), dim3(1024), 0, cur_stream(), ids, n_pairs, n_exp, order, pos_of, gstart,
-                       tiles, cap);
+                       tiles, cap, tiles2, cap2);
     return launched();
 }
 
