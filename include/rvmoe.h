@@ -236,9 +236,10 @@ int rvm_counters_reset(void);
 
 /* Diagnostic builds only (compiled with RVM_PHASE_TRACE; other builds return hipErrorNotSupported):
  * copies the realtime-counter stamps (100 MHz, u64) of the last decode call to host memory of at
- * least 3 x 4096 x 8 x 8 bytes: [kernel][workgroup][point] for k_router (0: entry, 1: done),
- * k_gateup_decode (0: entry, 1: expert known, 2: first block terms formed, 3: h block ready, 4:
- * down terms stored) and k_down_fold (0: entry, 1: rows folded, 2: output stored). No counterpart
+ * least 3 x 4096 x 8 x 8 bytes: [kernel][workgroup][point] for k_router (0: entry, 1: done, 2: row
+ * and x loaded), k_gateup_decode (0: entry, 1: expert known, 2: first block terms formed, 3: h block
+ * ready, 4: down terms stored) and k_down_fold (0: entry, 1: rows folded, 2: output stored, 3: down
+ * terms loaded); the points "loaded" wait for the loads, in this build only. No counterpart
  * in the reference: it measures where a decode token's time goes across workgroups and XCDs. */
 int rvm_phase_trace(void *host, size_t bytes);
 

@@ -26,7 +26,7 @@ constexpr int GU_WAVES = 8;  // K split of the gate_up tile
 #ifdef RVM_PHASE_TRACE
 // k_gateup_decode (0): 0 entry, 1 expert known (workgroup 0: ranking done), 2 wave 0's block terms
 // formed (workgroup 0: ids and weights published), 3 h block ready, 4 down terms stored;
-// k_down_fold (1): 0 entry, 1 slot rows folded, 2 output stored
+// k_down_fold (1): 0 entry, 1 slot rows folded, 2 output stored, 3 down terms loaded
 namespace {
 __device__ unsigned long long g_stamp[2 * TRACE_WG * TRACE_PT];
 }  // namespace
@@ -270,6 +270,7 @@ __global__ __launch_bounds__(256) void k_down_fold(const float *__restrict__ dte
 #pragma unroll
         for (int t = 0; t < T; ++t) v[t] = dterm[((size_t)hr * T + t) * d + row];
     }
+    RVM_STAMP_LOADED(g_stamp, 1, 3);
     float acc = 0.0f;
 #pragma unroll
     for (int t = 0; t < T; ++t) acc = acc + v[t];

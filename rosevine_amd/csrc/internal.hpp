@@ -366,8 +366,16 @@ constexpr int TRACE_WG = 4096, TRACE_PT = 8;
         if (threadIdx.x == 0 && blockIdx.x < (unsigned)rvm::TRACE_WG)                                     \
             (arr)[((k) * rvm::TRACE_WG + blockIdx.x) * rvm::TRACE_PT + (s)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
+// the same after every memory operation issued so far has completed (a wait that only the
+// diagnostic build has)
+#define RVM_STAMP_LOADED(arr, k, s)       \
+    do {                                  \
+        __builtin_amdgcn_s_waitcnt(0);    \
+        RVM_STAMP(arr, k, s);             \
+    } while (0)
 #else
 #define RVM_STAMP(arr, k, s) ((void)0)
+#define RVM_STAMP_LOADED(arr, k, s) ((void)0)
 #endif
 // Copy the stamps of k_router ([1][TRACE_WG][TRACE_PT]) and of k_gateup_decode, k_down_fold
 // ([2][TRACE_WG][TRACE_PT]) to host memory; hipErrorNotSupported in other builds.

@@ -20,7 +20,8 @@ namespace rvm {
 
 #ifdef RVM_PHASE_TRACE
 namespace {
-__device__ unsigned long long g_stamp[TRACE_WG * TRACE_PT];  // k_router: 0 entry, 1 done
+// k_router: 0 entry, 1 done, 2 row and x loaded (statistics workgroups)
+__device__ unsigned long long g_stamp[TRACE_WG * TRACE_PT];
 }  // namespace
 #endif
 
@@ -113,6 +114,7 @@ __global__ __launch_bounds__(RWAVES * 64) void k_router(const float *__restrict_
     for (int i = 0; i < F4; ++i) wv[i] = w4[i];
     float4 xv[F4];
     load_x_chunk<F4>(x, lane, xf, xv);
+    RVM_STAMP_LOADED(g_stamp, 0, 2);
     if (have) {
         const double2 st = row_stats<F4>(wv, xv, lane);
         if (lane == 0) stats[e] = st;

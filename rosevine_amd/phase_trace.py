@@ -26,9 +26,11 @@ from . import hip, moe, synth
 
 TRACE_WG, TRACE_PT = 4096, 8
 
-# (kernel index, point, label, workgroup range: "all", "tiles" (gate/up workgroups 1..), "wg0")
+# (kernel index, point, label, workgroups: "all", "stats" (the router's statistics workgroups),
+# "tiles" (gate/up workgroups 1..), "wg0")
 POINTS = [
     (0, 0, "k_router entry", "all"),
+    (0, 2, "k_router: router row and x loaded (statistics workgroups)", "stats"),
     (0, 1, "k_router done (statistics or Q8_0 blocks stored)", "all"),
     (1, 0, "k_gateup_decode entry", "all"),
     (1, 1, "tile: expert known (ranking done)", "tiles"),
@@ -38,6 +40,7 @@ POINTS = [
     (1, 1, "workgroup 0: ranking and certificate done", "wg0"),
     (1, 2, "workgroup 0: ids and weights published", "wg0"),
     (2, 0, "k_down_fold entry", "all"),
+    (2, 3, "k_down_fold: down terms loaded", "all"),
     (2, 1, "k_down_fold: slot rows folded", "all"),
     (2, 2, "k_down_fold: output stored", "all"),
 ]
@@ -88,6 +91,8 @@ def table(s: np.ndarray, E: int, K: int, D: int, FF: int) -> None:
         v = s[k, :sizes[k], p]
         if rng == "tiles":
             v = v[1:]
+        elif rng == "stats":
+            v = v[:E]
         elif rng == "wg0":
             v = v[:1]
         us = (v - t0) * 0.01
