@@ -441,20 +441,24 @@ __device__ bool exact_candidates(SelShared<F4, NW> &sh, const float *__restrict_
             }
     };
     float acc = -0.0f;
-    auto fold = [&](int buf) {
+    auto fold = [&](int buf) {  // the next 32 products are read from LDS while these are added
         if (w != 0) return;
         const float4 *pr = (const float4 *)(sh.P + buf * CM * PP + min(lane, nc - 1) * PP);
+        constexpr int G = CK / 32;
+        float4 v[2][8];
 #pragma unroll
-        for (int g = 0; g < CK / 32; ++g) {
-            float4 v[8];
+        for (int j = 0; j < 8; ++j) v[0][j] = pr[j];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = pr[g * 8 + j];
+        for (int g = 0; g < G; ++g) {
+            if (g + 1 < G)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[(g + 1) & 1][j] = pr[(g + 1) * 8 + j];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                acc = acc + v[j].x;
-                acc = acc + v[j].y;
-                acc = acc + v[j].z;
-                acc = acc + v[j].w;
+                acc = acc + v[g & 1][j].x;
+                acc = acc + v[g & 1][j].y;
+                acc = acc + v[g & 1][j].z;
+                acc = acc + v[g & 1][j].w;
             }
         }
     };
