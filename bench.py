@@ -358,7 +358,7 @@ def other_workload(args) -> int:
                 if sel and kind != sel:
                     continue
                 hip.kv_store(kv_new, kv_new, kc, vc, 1, nkv, hd, p0, cap, v_off=nkv * hd * 4)
-                hip.attention_split(q, kc, vc, out, part, 1, nh, nkv, hd, p0, cap, win, target)
+                hip.attention_split(q, kc, vc, out, part, 1, nh, nkv, hd, p0, cap, win, target, args.attn_min_chunk)
 
         reps = 50
         one_token(None)  # eager once: the launcher's per-kernel occupancy queries happen outside capture
@@ -439,6 +439,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-stack", action="store_true", help="skip the 30-layer (cache-cold) context figure")
+    ap.add_argument("--attn-min-chunk", type=int, default=64, help="attn: keys per chunk at least (the reference's 64)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--workload", default="decode", choices=["decode", "prefill512", "ragged32", "stack30", "q4gemv", "attn"],
                     help="decode (default, the headline line); prefill512: one layer over 512 tokens; ragged32: "

@@ -35,6 +35,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int v2i_t __attribute__((ext_vector_type(2)));
 
 struct __attribute__((packed, aligned(2))) Q8Half {  // 8 quants of a Q8_0 block
     uint32_t q[2];
@@ -398,6 +399,360 @@ __global__ __launch_bounds__(AT_WAVES * 64) void k_attn_split(
     }
 }
 
+// ---- Streaming split-K for head dimensions 256 and 512 (nb = 8 or 16 Q8_0 blocks per row) ----
+// A workgroup of 8 waves takes one tile (token, kv head, chunk) with up to 16 query heads of that kv
+// head, so that every key and value row of the tile is read once. The tile's keys go in stages of
+// 32, copied from HBM straight into LDS (global_load_lds, 1 KB of two or four whole rows per
+// instruction) through a ring of ST_RING stages: ST_RING - 1 stages are in flight while one is
+// computed, and each wave waits (vmcnt) only for the copies of the stage it needs next. A stage
+// sits in LDS as [K/V][key][16-byte piece p ^ key] (piece p holds half of block p / 2's quants, read
+// from the ring rows at 2-byte alignment; the XOR puts the same piece of 16 keys on distinct banks)
+// and the block scales as the dwords that start at them (low half), [K/V][key][block].
+//  - scores: v_mfma_f32_16x16x32_bf16, heads x 16 keys over one block (q as three exact bf16 parts,
+//    the key quants exact in bf16), scaled by the key's block scale; wave w takes key group w & 1
+//    and a quarter of the blocks, and the four partial scores meet in LDS;
+//  - softmax: wave w keeps heads 2 w and 2 w + 1 (lane = head parity, key): their running max and
+//    sum, and writes the stage's p and the rescale factor to LDS;
+//  - values: v_mfma_f32_16x16x32_bf16 with A = p * d_v (heads x 32 keys, three exact bf16 parts)
+//    and B = the value quants of 32 keys x 16 dimensions, read transposed out of LDS
+//    (ds_read_b64_tr_b8: each 16-lane group turns 8 keys x 8 bytes into 8 dimensions x 8 keys);
+//    wave w owns the dimensions of blocks w, w + 8, so no merge is needed.
+constexpr int ST_WAVES = 8;
+constexpr int ST_KEYS = 32;  // keys per stage
+constexpr int ST_RING = 4;   // stages resident in LDS
+constexpr int ST_PP = 36;    // row pitch of the p rows in LDS (floats)
+
+template <int NB>
+struct StreamShape {
+    static constexpr int HD = 32 * NB;
+    static constexpr int ROW = NB * Q8_BLOCK;
+    static constexpr int QBYTES = 2 * ST_KEYS * HD;      // quants of a stage, K then V
+    static constexpr int SBYTES = 2 * NB * ST_KEYS * 4;  // scale dwords of a stage
+    static constexpr int STAGE = QBYTES + SBYTES;
+    static constexpr int NQ = NB / 4;  // 16-byte copies per wave and stage
+    static constexpr int NS = NB / 8;  // 4-byte copies per wave and stage
+    static constexpr int NI = NQ + NS;
+    static constexpr int SBW = NB / 4;  // blocks per wave in the scores
+    static constexpr int VBW = NB / 8;  // blocks per wave in the values
+    static constexpr int LDS = ST_RING * STAGE + (4 * 16 * ST_KEYS + 16 * ST_PP + 2 * 16) * 4;
+    static_assert(LDS <= 163840, "LDS");
+};
+
+// s_waitcnt with vmcnt = n and no wait on the other counters (gfx9 encoding)
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+typedef __attribute__((address_space(3))) v2i_t lds_v2i_t;
+
+// Copies to LDS (global_load_lds): lane l's 16 (4) bytes at src go to LDS address lds + 16 l (4 l),
+// lds the same in every lane. Issued through asm so that the compiler, which cannot tell the ring's
+// stages apart, adds no wait for them before LDS reads: the kernel counts them itself (vmcnt).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_copy16(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy4(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p);
+}
+
+__device__ __forceinline__ bf16x8 q8x8_bf16(uint32_t a, uint32_t b) {
+    uint32_t k[4];
+    q8_bf16(a, k[0], k[1]);
+    q8_bf16(b, k[2], k[3]);
+    return __builtin_bit_cast(bf16x8, uint4{k[0], k[1], k[2], k[3]});
+}
+
+// x as three bf16 parts whose sum is x exactly (each part the rounding of the residual before it)
+__device__ __forceinline__ void split3_bf16(const float (&x)[8], bf16x8 (&a)[3]) {
+    uint32_t pk[3][4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        f32x2 r = {x[e], x[e + 1]};
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const bf16x2 b = __builtin_convertvector(r, bf16x2);
+            pk[k][e / 2] = __builtin_bit_cast(uint32_t, b);
+            r -= __builtin_convertvector(b, f32x2);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) a[k] = __builtin_bit_cast(bf16x8, uint4{pk[k][0], pk[k][1], pk[k][2], pk[k][3]});
+}
+
+// e^d for d <= 0 as 2^(d log2 e) on the hardware exp2 (0 for d = -inf)
+__device__ __forceinline__ float exp_le0(float d) { return __builtin_amdgcn_exp2f(d * 1.44269504088896341f); }
+
+// max and sum over the 32 lanes of a half-wave: the 16-lane DPP exchanges, then the other row's
+// result through a swizzle (every lane ends with the same bits)
+__device__ __forceinline__ float half32_max(float v) {
+    v = row16_max_f(v);
+    return maxf_bits(v, swz_xor16(__builtin_bit_cast(uint32_t, v)));
+}
+__device__ __forceinline__ float half32_sum(float v) {
+    v = row16_sum_f(v);
+    return v + __builtin_bit_cast(float, swz_xor16(__builtin_bit_cast(uint32_t, v)));
+}
+
+template <int NB>
+__global__ __launch_bounds__(ST_WAVES * 64) void k_attn_stream(
+    const float *__restrict__ q, const uint8_t *__restrict__ kc, const uint8_t *__restrict__ vc,
+    float *__restrict__ out, float *__restrict__ part, int n_tok, int n_head, int n_kv, int G, int p0, int cap,
+    int window, int n_chunks) {
+    using Sh = StreamShape<NB>;
+    constexpr int HD = Sh::HD, SBW = Sh::SBW, VBW = Sh::VBW, PMASK = 2 * NB - 1;
+    __shared__ __attribute__((aligned(16))) uint8_t ring[ST_RING * Sh::STAGE];
+    __shared__ __attribute__((aligned(16))) float red[4 * 16 * ST_KEYS];  // [block quarter][head][key]
+    __shared__ __attribute__((aligned(16))) float pl[16 * ST_PP];          // [head][key]: the stage's p
+    __shared__ __attribute__((aligned(16))) float hcorr[16], hsum[16];
+    const int lane = threadIdx.x & 63, lr = lane & 15, jg = lane >> 4, lk = lane & 31;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // workgroup -> (tile, head group) as in k_attn_split
+    const int S = (n_head / n_kv) / G;
+    const int xcd = blockIdx.x & 7, rest = blockIdx.x >> 3;
+    const int sg = rest % S;
+    const long T = (long)(rest / S) * 8 + xcd;
+    if (T >= (long)n_tok * n_kv * n_chunks) return;
+    const int c = (int)(T % n_chunks);
+    const int tg = (int)(T / n_chunks);
+    const int g = tg % n_kv, t = tg / n_kv;
+    const int h0 = g * (n_head / n_kv) + sg * G;
+    const int pos = p0 + t;
+    const int lo = window > 0 ? max(0, pos + 1 - window) : 0;
+    const int len = pos - lo + 1;
+    const int per = (len + n_chunks - 1) / n_chunks;
+    const int k0 = lo + c * per, k1 = min(pos + 1, k0 + per);
+    const int nkeys = max(0, k1 - k0), nst = (nkeys + ST_KEYS - 1) / ST_KEYS;
+    const size_t slot_bytes = (size_t)n_kv * Sh::ROW;
+    const int slot0 = k0 % cap;
+    const uint8_t *kg = kc + (size_t)g * Sh::ROW, *vg = vc + (size_t)g * Sh::ROW;
+
+    // the copies of stage s into its ring slot. Every wave issues exactly NI copy instructions per
+    // stage, stages past the tile included (those repeat one row, which stays in the caches), so that
+    // the waits count stages; keys past the tile repeat its last key. Copy i of this lane: the key,
+    // K or V, and the byte offset in the row are the same in every stage.
+    int ckey[Sh::NI];
+    const uint8_t *crow[Sh::NI];  // row base of the key's slot in stage 0, K or V
+    uint32_t coff[Sh::NI];
+#pragma unroll
+    for (int i = 0; i < Sh::NQ; ++i) {
+        const int P = (w * Sh::NQ + i) * 64 + lane;  // 16-byte slot of the stage: [K/V][key][slot]
+        const int key = (P / (2 * NB)) % ST_KEYS, j = (P & PMASK) ^ (key & PMASK);  // the piece it holds
+        ckey[i] = key;
+        crow[i] = P / (64 * NB) ? vg : kg;
+        coff[i] = Q8_BLOCK * (j >> 1) + 2 + 16 * (j & 1);
+    }
+#pragma unroll
+    for (int i = 0; i < Sh::NS; ++i) {
+        const int P = (w * Sh::NS + i) * 64 + lane;  // scale dword of the stage: [K/V][key][block]
+        ckey[Sh::NQ + i] = (P / NB) % ST_KEYS;
+        crow[Sh::NQ + i] = P / (32 * NB) ? vg : kg;
+        coff[Sh::NQ + i] = Q8_BLOCK * (P % NB);  // the dword starting at the block's scale
+    }
+    const uint32_t ring0 = lds_addr(ring);
+    auto issue = [&](int s) {
+        const uint32_t base = ring0 + (s % ST_RING) * Sh::STAGE;
+        const int kb = s * ST_KEYS;
+        const uint8_t *src[Sh::NI];
+        if (kb + ST_KEYS <= nkeys && slot0 + kb + ST_KEYS <= cap) {  // whole stage, no wrap
+            const size_t adv = (size_t)(slot0 + kb) * slot_bytes;
+#pragma unroll
+            for (int i = 0; i < Sh::NI; ++i) src[i] = crow[i] + adv + ((size_t)ckey[i] * slot_bytes + coff[i]);
+        } else {
+            const bool real = s < nst;
+            const int last = real ? min(ST_KEYS, nkeys - kb) - 1 : 0;
+#pragma unroll
+            for (int i = 0; i < Sh::NI; ++i) {
+                int sl = slot0 + (real ? kb + min(ckey[i], last) : 0);
+                sl = sl >= cap ? sl - cap : sl;
+                src[i] = crow[i] + (size_t)sl * slot_bytes + coff[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < Sh::NQ; ++i) lds_copy16(src[i], base + (w * Sh::NQ + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < Sh::NS; ++i)
+            lds_copy4(src[Sh::NQ + i], base + Sh::QBYTES + (w * Sh::NS + i) * 256);
+    };
+
+    // the queries and stage 0 first: 16 rows of HD floats (heads past G repeat head h0) into the last
+    // ring slot, which the first stages leave free; stages 1 and 2 once those have landed, so that the
+    // first stage of every workgroup is not queued behind the next ones
+    {
+        const uint32_t qbase = ring0 + (ST_RING - 1) * Sh::STAGE;
+        const float *qrow = q + ((size_t)t * n_head + h0) * HD;
+#pragma unroll
+        for (int i = 0; i < Sh::NQ; ++i) {
+            const int P = (w * Sh::NQ + i) * 64 + lane;  // 16-byte piece of the 16 x HD floats
+            const int hh = P / (HD / 4), e = P % (HD / 4);
+            lds_copy16(qrow + (size_t)(hh < G ? hh : 0) * HD + 4 * e, qbase + (w * Sh::NQ + i) * 1024);
+        }
+    }
+    issue(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    __syncthreads();
+#pragma unroll
+    for (int s = 1; s < ST_RING - 1; ++s) issue(s);
+
+    // the scores' share of this wave: key group kq, blocks SBW bq .. SBW bq + SBW - 1; q fragments
+    // (A: head lr, elements 8 jg .. + 7 of each block) as three bf16 parts
+    const int kq = w & 1, bq = w >> 1;
+    bf16x8 qa[SBW][3];
+    {
+        const float *qs = (const float *)(ring + (ST_RING - 1) * Sh::STAGE);
+#pragma unroll
+        for (int i = 0; i < SBW; ++i) {
+            const int b = SBW * bq + i;
+            const bool qok = lr < G;
+            const float4 *qr = (const float4 *)(qs + lr * HD + b * QK + 8 * jg);
+            const float4 x0 = qr[0], x1 = qr[1];
+            const float x[8] = {qok ? x0.x : 0.0f, qok ? x0.y : 0.0f, qok ? x0.z : 0.0f, qok ? x0.w : 0.0f,
+                                qok ? x1.x : 0.0f, qok ? x1.y : 0.0f, qok ? x1.z : 0.0f, qok ? x1.w : 0.0f};
+            split3_bf16(x, qa[i]);
+        }
+    }
+
+    // the softmax of heads hw = 2 w + lane / 32, key lk: running max and sum
+    const int hw = 2 * w + (lane >> 5);
+    float m = -INFINITY, lsum = 0.0f;
+    f32x4 acc[VBW][2];
+#pragma unroll
+    for (int i = 0; i < VBW; ++i) acc[i][0] = acc[i][1] = f32x4{0, 0, 0, 0};
+
+    for (int s = 0; s < nst; ++s) {
+        if (s > 0) {  // stage s + 1 stays in flight; stage 0 was waited for with the queries
+            __builtin_amdgcn_s_waitcnt(vmcnt_only((ST_RING - 3) * Sh::NI));
+            __syncthreads();  // the stage is in LDS for every wave; the slot of stage s - 2 is free
+            issue(s + ST_RING - 2);
+        }
+        const uint8_t *sb = ring + (s % ST_RING) * Sh::STAGE;
+        const uint32_t *scl = (const uint32_t *)(sb + Sh::QBYTES);
+        const int nk = min(ST_KEYS, nkeys - s * ST_KEYS);
+
+        // ---- scores: heads x keys 16 kq .. 16 kq + 15 over this wave's blocks
+        if (kq == 0 || nk > 16) {
+            const int kl = 16 * kq + lr;
+            f32x4 s4 = {0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < SBW; ++i) {
+                const int b = SBW * bq + i;
+                const int slot = (2 * b + (jg >> 1)) ^ (kl & PMASK);
+                const uint2 kw = *(const uint2 *)(sb + (kl * 2 * NB + slot) * 16 + 8 * (jg & 1));
+                const bf16x8 bk = q8x8_bf16(kw.x, kw.y);
+                f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[i][0], bk, f32x4{0, 0, 0, 0}, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[i][1], bk, d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[i][2], bk, d, 0, 0, 0);
+                const float dk = h2f((uint16_t)scl[kl * NB + b]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s4[r] = fmaf(dk, d[r], s4[r]);
+            }
+            float *rw = red + bq * 16 * ST_KEYS;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) rw[(4 * jg + r) * ST_KEYS + kl] = s4[r];
+        }
+        __syncthreads();
+
+        // ---- online softmax of heads 2 w, 2 w + 1 over the stage's keys (one key per lane)
+        {
+            const int hh = hw < 16 ? hw : 0;
+            float sv = ((red[hh * ST_KEYS + lk] + red[(16 + hh) * ST_KEYS + lk]) + red[(32 + hh) * ST_KEYS + lk]) +
+                       red[(48 + hh) * ST_KEYS + lk];
+            sv = lk < nk ? sv : -INFINITY;
+            const float mn = fmaxf(m, half32_max(sv));
+            const float corr = exp_le0(m - mn);  // 0 while m = -inf
+            const float p = exp_le0(sv - mn);    // 0 for keys past the stage
+            lsum = lsum * corr + half32_sum(p);
+            m = mn;
+            if (hw < 16) {
+                pl[hw * ST_PP + lk] = hw < G ? p : 0.0f;
+                if (lk == 0) hcorr[hw] = corr;
+            }
+        }
+        __syncthreads();
+
+        // ---- values: heads x the 32 dimensions of each of the wave's blocks
+        {
+            const float4 *pr = (const float4 *)(pl + lr * ST_PP + 8 * jg);
+            const float4 pa = pr[0], pb = pr[1];
+            const float p[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+            const float4 cr = *(const float4 *)(hcorr + 4 * jg);  // rows 4 jg .. 4 jg + 3 of the MFMA output
+#pragma unroll
+            for (int i = 0; i < VBW; ++i)
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    acc[i][tt][0] *= cr.x;
+                    acc[i][tt][1] *= cr.y;
+                    acc[i][tt][2] *= cr.z;
+                    acc[i][tt][3] *= cr.w;
+                }
+#pragma unroll
+            for (int i = 0; i < VBW; ++i) {
+                const int b = w + ST_WAVES * i;
+                float x[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    x[e] = p[e] * h2f((uint16_t)scl[(ST_KEYS + 8 * jg + e) * NB + b]);
+                bf16x8 a[3];
+                split3_bf16(x, a);
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    // source row of this lane: key 8 jg + lr / 2, dimensions 32 b + 16 tt + 8 (lr & 1) .. + 7
+                    const int kl = 8 * jg + (lr >> 1);
+                    const int slot = (2 * b + tt) ^ (kl & PMASK);
+                    const uint8_t *src = sb + ((ST_KEYS + kl) * 2 * NB + slot) * 16 + 8 * (lr & 1);
+                    const v2i_t vt = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t *)src);
+                    const bf16x8 bv = q8x8_bf16((uint32_t)vt.x, (uint32_t)vt.y);
+                    acc[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], bv, acc[i][tt], 0, 0, 0);
+                    acc[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], bv, acc[i][tt], 0, 0, 0);
+                    acc[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], bv, acc[i][tt], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // the copies past the last stage land in LDS: none may be in flight when the workgroup ends
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+
+    // ---- results: lane (lr, jg) holds heads 4 jg + r, dimension 32 b + 16 tt + lr of each block
+    const size_t r0 = (size_t)t * n_head + h0;
+    if (hw < 16 && lk == 0) hsum[hw] = lsum;
+    __syncthreads();
+    if (n_chunks == 1) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int h = 4 * jg + r;
+            const float inv = 1.0f / hsum[h];
+            if (h < G)
+#pragma unroll
+                for (int i = 0; i < VBW; ++i)
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt)
+                        out[(r0 + h) * HD + 32 * (w + ST_WAVES * i) + 16 * tt + lr] = acc[i][tt][r] * inv;
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int h = 4 * jg + r;
+            if (h < G) {
+                float *pp = part + ((r0 + h) * n_chunks + c) * (size_t)(HD + 2);
+#pragma unroll
+                for (int i = 0; i < VBW; ++i)
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) pp[2 + 32 * (w + ST_WAVES * i) + 16 * tt + lr] = acc[i][tt][r];
+            }
+        }
+        if (hw < G && lk == 0) {
+            float *pp = part + ((r0 + hw) * n_chunks + c) * (size_t)(HD + 2);
+            pp[0] = m;
+            pp[1] = lsum;
+        }
+    }
+}
+
 // out[i][d] = sum_c e^(m_c - M) acc_c[d] / sum_c e^(m_c - M) l_c with M = max_c m_c; an empty chunk
 // (m = -inf, l = 0) adds nothing (the reference's merge, runtime/hip/rvhip.hip:376-394).
 // Workgroup (row, 64 dimensions), lane = dimension: wave w folds chunks w, w + 4, ... in one pass
@@ -573,8 +928,28 @@ int attn_group(int n_tok, int n_head, int n_kv, int n_chunks) {
     return gt;
 }
 
+// The streaming kernel's head group: every query head of a kv head, or groups of 16 when there are
+// more (0 when it does not apply: another head dimension, or a count of heads 16 does not divide).
+inline int stream_group(int n_head, int n_kv, int hd) {
+    if (hd != 256 && hd != 512) return 0;
+    const int per_kv = n_head / n_kv;
+    return per_kv <= 16 ? per_kv : (per_kv % 16 == 0 ? 16 : 0);
+}
+
 int launch_attn(const float *q, const void *kc, const void *vc, float *out, float *part, int n_tok, int n_head,
                 int n_kv, int hd, int p0, int cap, int window, int n_chunks) {
+    if (const int G = stream_group(n_head, n_kv, hd)) {
+        const long wgs = attn_wgs(n_tok, n_head, n_kv, n_chunks, G);
+        RVM_CHECK(wgs <= 0x7fffffffL);
+        const uint8_t *k8 = (const uint8_t *)kc, *v8 = (const uint8_t *)vc;
+        if (hd == 512)
+            hipLaunchKernelGGL(k_attn_stream<16>, dim3((unsigned)wgs), dim3(ST_WAVES * 64), 0, cur_stream(), q, k8, v8,
+                               out, part, n_tok, n_head, n_kv, G, p0, cap, window, n_chunks);
+        else
+            hipLaunchKernelGGL(k_attn_stream<8>, dim3((unsigned)wgs), dim3(ST_WAVES * 64), 0, cur_stream(), q, k8, v8,
+                               out, part, n_tok, n_head, n_kv, G, p0, cap, window, n_chunks);
+        return launched();
+    }
     // heads per workgroup times dimensions per lane at most 64: the merge buffer's LDS
     const bool wide = hd > 256;
     const int gt = wide ? attn_group<8>(n_tok, n_head, n_kv, n_chunks) : attn_group<4>(n_tok, n_head, n_kv, n_chunks);

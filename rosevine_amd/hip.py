@@ -437,10 +437,11 @@ def q8_row_bytes(hd: int) -> int:
     return hd // QK * Q8_BLOCK
 
 
-def attention_chunks(n_tok: int, n_head: int, longest: int, target_blocks: int = ATTN_TARGET_BLOCKS) -> int:
-    """Key chunks per query head (runtime/src/hip.rs:486-490): ceil(keys / 64), at most
-    target_blocks / (tokens * heads) so that decode fills the device and prefill takes one chunk."""
-    by_keys = max(-(-longest // ATTN_MIN_CHUNK), 1)
+def attention_chunks(n_tok: int, n_head: int, longest: int, target_blocks: int = ATTN_TARGET_BLOCKS,
+                     min_chunk: int = ATTN_MIN_CHUNK) -> int:
+    """Key chunks per query head (runtime/src/hip.rs:486-490): ceil(keys / min_chunk) (64 there), at
+    most target_blocks / (tokens * heads) so that decode fills the device and prefill takes one chunk."""
+    by_keys = max(-(-longest // min_chunk), 1)
     by_blocks = max(target_blocks // max(n_tok * n_head, 1), 1)
     return min(by_keys, by_blocks)
 
@@ -488,11 +489,12 @@ def attn_combine(part: DevBuf, out: DevBuf, rows: int, hd: int, n_chunks: int) -
 
 
 def attention_split(q: DevBuf, kc: DevBuf, vc: DevBuf, out: DevBuf, part: DevBuf, n_tok: int, n_head: int, n_kv: int,
-                    hd: int, p0: int, cap: int, window: int, target_blocks: int = ATTN_TARGET_BLOCKS) -> int:
+                    hd: int, p0: int, cap: int, window: int, target_blocks: int = ATTN_TARGET_BLOCKS,
+                    min_chunk: int = ATTN_MIN_CHUNK) -> int:
     """Split-K attention as runtime/src/hip.rs:503-530: attention_chunks chunks per query head, the
     partials merged by rvh_attn_combine when there is more than one. part holds
     attention_split_scratch(..., target_blocks) floats. Returns the chunk count."""
-    chunks = attention_chunks(n_tok, n_head, _attn_longest(n_tok, p0, window), target_blocks)
+    chunks = attention_chunks(n_tok, n_head, _attn_longest(n_tok, p0, window), target_blocks, min_chunk)
     attn_split(q, kc, vc, out, part, n_tok, n_head, n_kv, hd, p0, cap, window, chunks)
     if chunks > 1:
         attn_combine(part, out, n_tok * n_head, hd, chunks)
