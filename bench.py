@@ -353,12 +353,17 @@ def other_workload(args) -> int:
         hip.sync()
         p0 = depth  # the token at position 16384 attends to 16385 keys (global) or 1024 (local)
 
+        chunks = {kind: hip.attention_chunks(1, nh, min(p0 + 1, win) if win else p0 + 1, target, args.attn_min_chunk)
+                  for kind, (nh, nkv, hd, win, cap) in cfgs.items()}
+
         def one_token(sel):
+            # per layer rvm_attn_decode: the new key/value row into the ring and split-K attention
+            # with its merge (the reference's kv_store, attention_split, attn_combine)
             for kind, nh, nkv, hd, win, cap, kc, vc, kv_new, q, out, part in layers:
                 if sel and kind != sel:
                     continue
-                hip.kv_store(kv_new, kv_new, kc, vc, 1, nkv, hd, p0, cap, v_off=nkv * hd * 4)
-                hip.attention_split(q, kc, vc, out, part, 1, nh, nkv, hd, p0, cap, win, target, args.attn_min_chunk)
+                hip.attn_decode(q, kv_new, kv_new, kc, vc, out, part, nh, nkv, hd, p0, cap, win, chunks[kind],
+                                v_off=nkv * hd * 4)
 
         reps = 50
         one_token(None)  # eager once: the launcher's per-kernel occupancy queries happen outside capture
@@ -402,7 +407,9 @@ def other_workload(args) -> int:
                      "warmup": reps, "ms_per_step": round(ms, 6), "dtype": "Q8_0 K/V x f32 q -> f32 (bf16x3 MFMA scores)",
                      "data": "synthetic (random Q8_0 rings, N(0,0.2) queries)", "scaling": "weak",
                      "config": {"workload": "attn", "depth": depth, "layers": per,
-                                "chunk_policy": f"runtime/src/hip.rs:486-490 with target {target} (the reference's 1024)",
+                                "chunk_policy": f"runtime/src/hip.rs:486-490 with target {target} (the reference's 1024) "
+                                                f"and chunks of at least {args.attn_min_chunk} keys (the reference's 64)",
+                                "chunks": chunks, "entry": "rvm_attn_decode (kv store + split + merge, 2 launches)",
                                 "reference_attn_core_ms": {"d16384": 7.8, "global_part": 5.7,
                                                            "note": "reference host GPU, sync mode "
                                                                    "(docs/split-k-attention.md:75)"}},
@@ -439,7 +446,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-stack", action="store_true", help="skip the 30-layer (cache-cold) context figure")
-    ap.add_argument("--attn-min-chunk", type=int, default=64, help="attn: keys per chunk at least (the reference's 64)")
+    ap.add_argument("--attn-min-chunk", type=int, default=32,
+                    help="attn: keys per chunk at least (the reference's policy has 64)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--workload", default="decode", choices=["decode", "prefill512", "ragged32", "stack30", "q4gemv", "attn"],
                     help="decode (default, the headline line); prefill512: one layer over 512 tokens; ragged32: "

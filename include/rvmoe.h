@@ -83,6 +83,13 @@ int rvh_attn_split(const float *q, const void *kc, const void *vc, float *out, f
 /* Merge rows * n_chunks partials of rvh_attn_split into rows outputs of hd. n_chunks > 1.
  * rvhip.h:66-67. */
 int rvh_attn_combine(const float *part, float *out, int rows, int hd, int n_chunks);
+/* One decode token's attention core: rvh_kv_store of its key and value rows ([n_kv][hd] f32) into
+ * slot pos % cap, then rvh_attn_split over keys lo .. pos with n_chunks chunks and, for n_chunks > 1,
+ * rvh_attn_combine (part as there) -- the ring bytes and out bit for bit that sequence, which the
+ * reference runs as three calls (runtime/src/hip_exec.rs:743-760). No counterpart symbol in rvhip.h:
+ * for hd 256 and 512 the store happens inside the split kernel, one launch fewer per layer. */
+int rvm_attn_decode(const float *q, const float *k, const float *v, void *kc, void *vc, float *out, float *part,
+                    int n_head, int n_kv, int hd, int pos, int cap, int window, int n_chunks);
 
 /* ---- Additive MoE entry points (no counterpart symbol in rvhip.h) ---- */
 

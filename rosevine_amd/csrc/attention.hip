@@ -498,11 +498,17 @@ __device__ __forceinline__ float half32_sum(float v) {
     return v + __builtin_bit_cast(float, swz_xor16(__builtin_bit_cast(uint32_t, v)));
 }
 
+//
+// With kin / vin set (one decode token, n_tok = 1) the kernel also stores that token's key and value
+// rows: the workgroups whose chunk holds position p0 quantise them (bit for bit k_kv_store's Q8_0),
+// head group 0 writes them to ring slot p0 % cap, and each writes them over the stale slot's copy
+// in its LDS stage before computing it (the value scales of the stage's later keys, copies of that
+// slot, are set to 0: those keys weigh 0).
 template <int NB>
 __global__ __launch_bounds__(ST_WAVES * 64) void k_attn_stream(
-    const float *__restrict__ q, const uint8_t *__restrict__ kc, const uint8_t *__restrict__ vc,
-    float *__restrict__ out, float *__restrict__ part, int n_tok, int n_head, int n_kv, int G, int p0, int cap,
-    int window, int n_chunks) {
+    const float *__restrict__ q, uint8_t *__restrict__ kc, uint8_t *__restrict__ vc, float *__restrict__ out,
+    float *__restrict__ part, int n_tok, int n_head, int n_kv, int G, int p0, int cap, int window, int n_chunks,
+    const float *__restrict__ kin, const float *__restrict__ vin) {
     using Sh = StreamShape<NB>;
     constexpr int HD = Sh::HD, SBW = Sh::SBW, VBW = Sh::VBW, PMASK = 2 * NB - 1;
     __shared__ __attribute__((aligned(16))) uint8_t ring[ST_RING * Sh::STAGE];
@@ -579,6 +585,19 @@ __global__ __launch_bounds__(ST_WAVES * 64) void k_attn_stream(
             lds_copy4(src[Sh::NQ + i], base + Sh::QBYTES + (w * Sh::NS + i) * 256);
     };
 
+    // the new token's key and value (fused store): half-wave (w, lane / 32) quantises blocks
+    // 16 i + 2 w + lane / 32 of [K blocks, V blocks], element lane % 32
+    constexpr int NPASS = NB / 8;
+    const bool fuse = kin != nullptr && k0 <= pos && pos < k1;
+    float fx[NPASS];
+    if (fuse) {
+#pragma unroll
+        for (int i = 0; i < NPASS; ++i) {
+            const int B = 16 * i + 2 * w + (lane >> 5);
+            fx[i] = (B < NB ? kin : vin)[(size_t)g * HD + QK * (B % NB) + lk];
+        }
+    }
+
     // the queries and stage 0 first: 16 rows of HD floats (heads past G repeat head h0) into the last
     // ring slot, which the first stages leave free; stages 1 and 2 once those have landed, so that the
     // first stage of every workgroup is not queued behind the next ones
@@ -597,6 +616,27 @@ __global__ __launch_bounds__(ST_WAVES * 64) void k_attn_stream(
     __syncthreads();
 #pragma unroll
     for (int s = 1; s < ST_RING - 1; ++s) issue(s);
+    // the fused token's row (its stores come after the copies of stages 1 and 2; the waits below
+    // count loads, which complete in order, so a store still in flight only delays them)
+    int fq[NPASS];
+    uint16_t fd[NPASS];
+    if (fuse) {
+        uint8_t *slotp = nullptr;
+        const int sp = p0 % cap;
+#pragma unroll
+        for (int i = 0; i < NPASS; ++i) {
+            const int B = 16 * i + 2 * w + (lane >> 5);
+            fq[i] = quant_q8_half(fx[i], &fd[i]);
+            if (sg == 0) {  // the ring row, as k_kv_store writes it
+                slotp = (B < NB ? kc : vc) + ((size_t)sp * n_kv + g) * Sh::ROW + Q8_BLOCK * (B % NB);
+                slotp[2 + lk] = (uint8_t)(int8_t)fq[i];
+                if (lk == 0) {
+                    slotp[0] = (uint8_t)(fd[i] & 0xff);
+                    slotp[1] = (uint8_t)(fd[i] >> 8);
+                }
+            }
+        }
+    }
 
     // the scores' share of this wave: key group kq, blocks SBW bq .. SBW bq + SBW - 1; q fragments
     // (A: head lr, elements 8 jg .. + 7 of each block) as three bf16 parts
@@ -632,6 +672,22 @@ __global__ __launch_bounds__(ST_WAVES * 64) void k_attn_stream(
         const uint8_t *sb = ring + (s % ST_RING) * Sh::STAGE;
         const uint32_t *scl = (const uint32_t *)(sb + Sh::QBYTES);
         const int nk = min(ST_KEYS, nkeys - s * ST_KEYS);
+        if (fuse && s == (pos - k0) / ST_KEYS) {  // the stage holding the new token: its row into LDS
+            uint8_t *st = ring + (s % ST_RING) * Sh::STAGE;
+            uint32_t *stsc = (uint32_t *)(st + Sh::QBYTES);
+            const int kp = (pos - k0) % ST_KEYS;
+#pragma unroll
+            for (int i = 0; i < NPASS; ++i) {
+                const int B = 16 * i + 2 * w + (lane >> 5), which = B / NB, b = B % NB;
+                const int slot = (2 * b + (lk >> 4)) ^ (kp & PMASK);
+                st[((which * ST_KEYS + kp) * 2 * NB + slot) * 16 + (lk & 15)] = (uint8_t)(int8_t)fq[i];
+                if (lk == 0) stsc[(which * ST_KEYS + kp) * NB + b] = fd[i];
+            }
+            // the later keys of the stage repeat the stale slot: a value scale of 0 keeps them finite
+            const int dk = kp + 1 + (int)threadIdx.x / NB, db = (int)threadIdx.x % NB;
+            if (dk < ST_KEYS) stsc[(ST_KEYS + dk) * NB + db] = 0u;
+            __syncthreads();
+        }
 
         // ---- scores: heads x keys 16 kq .. 16 kq + 15 over this wave's blocks
         if (kq == 0 || nk > 16) {
@@ -936,20 +992,27 @@ inline int stream_group(int n_head, int n_kv, int hd) {
     return per_kv <= 16 ? per_kv : (per_kv % 16 == 0 ? 16 : 0);
 }
 
+int launch_stream(const float *q, const void *kc, const void *vc, float *out, float *part, int n_tok, int n_head,
+                  int n_kv, int hd, int p0, int cap, int window, int n_chunks, int G, const float *kin,
+                  const float *vin) {
+    const long wgs = attn_wgs(n_tok, n_head, n_kv, n_chunks, G);
+    RVM_CHECK(wgs <= 0x7fffffffL);
+    // the rings are written only with kin / vin set (rvm_attn_decode, whose rings are writable)
+    uint8_t *k8 = (uint8_t *)kc, *v8 = (uint8_t *)vc;
+    if (hd == 512)
+        hipLaunchKernelGGL(k_attn_stream<16>, dim3((unsigned)wgs), dim3(ST_WAVES * 64), 0, cur_stream(), q, k8, v8, out,
+                           part, n_tok, n_head, n_kv, G, p0, cap, window, n_chunks, kin, vin);
+    else
+        hipLaunchKernelGGL(k_attn_stream<8>, dim3((unsigned)wgs), dim3(ST_WAVES * 64), 0, cur_stream(), q, k8, v8, out,
+                           part, n_tok, n_head, n_kv, G, p0, cap, window, n_chunks, kin, vin);
+    return launched();
+}
+
 int launch_attn(const float *q, const void *kc, const void *vc, float *out, float *part, int n_tok, int n_head,
                 int n_kv, int hd, int p0, int cap, int window, int n_chunks) {
-    if (const int G = stream_group(n_head, n_kv, hd)) {
-        const long wgs = attn_wgs(n_tok, n_head, n_kv, n_chunks, G);
-        RVM_CHECK(wgs <= 0x7fffffffL);
-        const uint8_t *k8 = (const uint8_t *)kc, *v8 = (const uint8_t *)vc;
-        if (hd == 512)
-            hipLaunchKernelGGL(k_attn_stream<16>, dim3((unsigned)wgs), dim3(ST_WAVES * 64), 0, cur_stream(), q, k8, v8,
-                               out, part, n_tok, n_head, n_kv, G, p0, cap, window, n_chunks);
-        else
-            hipLaunchKernelGGL(k_attn_stream<8>, dim3((unsigned)wgs), dim3(ST_WAVES * 64), 0, cur_stream(), q, k8, v8,
-                               out, part, n_tok, n_head, n_kv, G, p0, cap, window, n_chunks);
-        return launched();
-    }
+    if (const int G = stream_group(n_head, n_kv, hd))
+        return launch_stream(q, kc, vc, out, part, n_tok, n_head, n_kv, hd, p0, cap, window, n_chunks, G, nullptr,
+                             nullptr);
     // heads per workgroup times dimensions per lane at most 64: the merge buffer's LDS
     const bool wide = hd > 256;
     const int gt = wide ? attn_group<8>(n_tok, n_head, n_kv, n_chunks) : attn_group<4>(n_tok, n_head, n_kv, n_chunks);
@@ -1005,6 +1068,22 @@ int rvh_attn_combine(const float *part, float *out, int rows, int hd, int n_chun
     hipLaunchKernelGGL(k_attn_combine, dim3(rows, (hd + 63) / 64), dim3(AT_WAVES * 64), 0, cur_stream(), part, out,
                        hd, n_chunks);
     return launched();
+}
+
+int rvm_attn_decode(const float *q, const float *k, const float *v, void *kc, void *vc, float *out, float *part,
+                    int n_head, int n_kv, int hd, int pos, int cap, int window, int n_chunks) {
+    RVM_CHECK(q && k && v && kc && vc && out && n_kv > 0 && n_head > 0 && n_head % n_kv == 0 && hd > 0 &&
+              hd % QK == 0 && hd <= AT_MAXHD && pos >= 0 && cap > 0 && window >= 0 && n_chunks > 0 &&
+              (n_chunks == 1 || part));
+    RVM_CHECK(attn_longest(1, pos, window) <= cap);
+    const int G = stream_group(n_head, n_kv, hd);
+    if (!G) {  // other shapes: the three reference operations in sequence
+        if (int rc = rvh_kv_store(k, v, kc, vc, 1, n_kv, hd, pos, cap)) return rc;
+        if (int rc = launch_attn(q, kc, vc, out, part, 1, n_head, n_kv, hd, pos, cap, window, n_chunks)) return rc;
+    } else if (int rc = launch_stream(q, kc, vc, out, part, 1, n_head, n_kv, hd, pos, cap, window, n_chunks, G, k, v)) {
+        return rc;
+    }
+    return n_chunks > 1 ? rvh_attn_combine(part, out, n_head, hd, n_chunks) : 0;
 }
 
 int rvh_attention(const float *q, const void *kc, const void *vc, float *out, float *scores, int n_tok, int n_head,

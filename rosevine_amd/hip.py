@@ -98,6 +98,7 @@ SIGNATURES = {
     "rvh_attention": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i]),
     "rvh_attn_split": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i]),
     "rvh_attn_combine": (_i, [_vp, _vp, _i, _i, _i]),
+    "rvm_attn_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i]),
     "rvm_set_stream": (_i, [_vp]),
     "rvm_stream_create": (_i, [C.POINTER(_vp)]),
     "rvm_stream_destroy": (_i, [_vp]),
@@ -486,6 +487,16 @@ def attn_split(q: DevBuf, kc: DevBuf, vc: DevBuf, out: DevBuf, part: DevBuf | No
 def attn_combine(part: DevBuf, out: DevBuf, rows: int, hd: int, n_chunks: int) -> None:
     check(lib().rvh_attn_combine(_need(part, rows * n_chunks * (hd + 2) * 4), _need(out, rows * hd * 4), rows, hd,
                                  n_chunks))
+
+
+def attn_decode(q: DevBuf, k: DevBuf, v: DevBuf, kc: DevBuf, vc: DevBuf, out: DevBuf, part: DevBuf | None,
+                n_head: int, n_kv: int, hd: int, pos: int, cap: int, window: int, n_chunks: int, k_off: int = 0,
+                v_off: int = 0) -> None:
+    """rvm_attn_decode: one decode token's key/value store and split-K attention (with the merge)."""
+    nq, nk, c = n_head * hd * 4, n_kv * hd * 4, cap * n_kv * q8_row_bytes(hd)
+    pp = _need(part, n_head * n_chunks * (hd + 2) * 4) if n_chunks > 1 else (part.at() if part else None)
+    check(lib().rvm_attn_decode(_need(q, nq), k.at(k_off, nk), v.at(v_off, nk), _need(kc, c), _need(vc, c),
+                                _need(out, nq), pp, n_head, n_kv, hd, pos, cap, window, n_chunks))
 
 
 def attention_split(q: DevBuf, kc: DevBuf, vc: DevBuf, out: DevBuf, part: DevBuf, n_tok: int, n_head: int, n_kv: int,

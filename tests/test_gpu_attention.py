@@ -184,3 +184,48 @@ def test_split_attention_against_f64_in_the_peaked_regime(gpu, orc):
         err = rel(got, want)
         print(f"[attn] peaked regime scale {scale}: rel {err:.2e}", flush=True)
         assert err <= 2.0 * published_one_pass[scale]
+
+
+@pytest.mark.parametrize("nh,nkv,hd,win,cap,pos,n_chunks", [
+    (16, 2, 512, 0, 6000, 5000, 64),     # the new key alone in stage 0 of the last chunk's 24 keys
+    (16, 2, 512, 0, 6000, 5000, 128),    # a chunk of one key (the new one); chunks past it empty
+    (16, 2, 512, 0, 6000, 5000, 16),     # the new key in stage 9 of its chunk
+    (16, 2, 512, 0, 6000, 5000, 1),      # one chunk: no merge
+    (16, 8, 256, 1024, 1028, 2000, 32),  # sliding window over a wrapped ring, 32-key chunks
+    (16, 8, 256, 1024, 1028, 2000, 16),  # the new key at the end of stage 1
+    (32, 2, 512, 0, 300, 250, 7),        # 16 heads of a kv head per workgroup, two head groups
+    (8, 4, 128, 0, 300, 250, 5),         # another head dimension: the three operations in sequence
+])
+def test_decode_entry_matches_store_split_and_merge(gpu, orc, nh, nkv, hd, win, cap, pos, n_chunks):
+    """rvm_attn_decode: the ring bytes and the output equal rvh_kv_store + rvh_attn_split +
+    rvh_attn_combine bit for bit. The token's ring slot starts as 0xff bytes (NaN scales), so a stale
+    copy of it that reached the computation would show."""
+    print(f"[attn decode] {nh}/{nkv}/{hd} win {win} cap {cap} pos {pos} chunks {n_chunks}", flush=True)
+    rng = np.random.default_rng(pos + n_chunks + hd)
+    kc, vc = q8_ring(orc, rng, cap, nkv, hd)
+    row = hd // QK * Q8B
+    sl = pos % cap
+    for c in (kc, vc):
+        c[sl * nkv * row:(sl + 1) * nkv * row] = 0xff
+    q = (rng.standard_normal(nh * hd) * 0.3).astype(np.float32)
+    kv = rng.standard_normal((2, nkv * hd)).astype(np.float32)
+    dq, dk, dv = dev(q), dev(kv[0]), dev(kv[1])
+    part = DevBuf(nh * n_chunks * (hd + 2) * 4)
+    # the three operations
+    kc1, vc1, out1 = dev(kc), dev(vc), DevBuf(nh * hd * 4)
+    hip.kv_store(dk, dv, kc1, vc1, 1, nkv, hd, pos, cap)
+    hip.attn_split(dq, kc1, vc1, out1, part, 1, nh, nkv, hd, pos, cap, win, n_chunks)
+    if n_chunks > 1:
+        hip.attn_combine(part, out1, nh, hd, n_chunks)
+    # the fused entry
+    kc2, vc2, out2 = dev(kc), dev(vc), DevBuf(nh * hd * 4)
+    hip.attn_decode(dq, dk, dv, kc2, vc2, out2, part, nh, nkv, hd, pos, cap, win, n_chunks)
+    assert np.array_equal(kc2.download(np.uint8, kc.size), kc1.download(np.uint8, kc.size))
+    assert np.array_equal(vc2.download(np.uint8, vc.size), vc1.download(np.uint8, vc.size))
+    got, want = out2.download(np.float32, nh * hd), out1.download(np.float32, nh * hd)
+    assert np.all(np.isfinite(got))
+    assert np.array_equal(got, want)
+    # and the oracle's attention over the stored ring
+    ref = orc.attention(q, kc1.download(np.uint8, kc.size), vc1.download(np.uint8, vc.size), nh, nkv, hd, cap, win,
+                        pos, 1)
+    assert rel(got, ref) < 1e-5
