@@ -370,6 +370,16 @@ def other_workload(args) -> int:
         hip.sync()
 
         def timed(sel) -> float:
+            if args.attn_eager:  # the same launches without graph capture (for kernel tracing)
+                one_token(sel)
+                hip.sync()
+                e0, e1 = hip.Event(), hip.Event()
+                e0.record()
+                for _ in range(reps):
+                    one_token(sel)
+                e1.record()
+                e1.synchronize()
+                return e0.elapsed_ms(e1) / reps
             # reps tokens as replays of one graph of GRAPH_TOKENS tokens (at most 900 kernel nodes)
             hip.Graph.begin()
             for _ in range(GRAPH_TOKENS):
@@ -410,6 +420,7 @@ def other_workload(args) -> int:
                                 "chunk_policy": f"runtime/src/hip.rs:486-490 with target {target} (the reference's 1024) "
                                                 f"and chunks of at least {args.attn_min_chunk} keys (the reference's 64)",
                                 "chunks": chunks, "entry": "rvm_attn_decode (kv store + split + merge, 2 launches)",
+                                "launch": "eager (host-bound)" if args.attn_eager else f"graphs of {GRAPH_TOKENS} tokens",
                                 "reference_attn_core_ms": {"d16384": 7.8, "global_part": 5.7,
                                                            "note": "reference host GPU, sync mode "
                                                                    "(docs/split-k-attention.md:75)"}},
@@ -446,6 +457,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-stack", action="store_true", help="skip the 30-layer (cache-cold) context figure")
+    ap.add_argument("--attn-eager", action="store_true",
+                    help="attn: launch the layers without graph capture (host-bound; for kernel tracing)")
     ap.add_argument("--attn-min-chunk", type=int, default=32,
                     help="attn: keys per chunk at least (the reference's policy has 64)")
     ap.add_argument("--seed", type=int, default=0)
