@@ -282,21 +282,37 @@ def other_workload(args) -> int:
                   ("ffn_gate", 2112, D), ("ffn_up", 2112, D), ("ffn_down", D, 2112)]
         head = ("head", 262144, D)
         rng = np.random.default_rng(args.seed)
+        # the inputs as in the layer: q, k, v (and the head) share the normed hidden row, gate and up
+        # share the normed attention output; attn_output and ffn_down take their own
+        xin = {kk: hip.DevBuf.from_array(rng.standard_normal(kk).astype(np.float32)) for kk in (D, 4096, 2112)}
+        xin["ffn"] = hip.DevBuf.from_array(rng.standard_normal(D).astype(np.float32))
         mats = {}
         for name, n_out, k in shapes + [head]:
             wbuf = hip.DevBuf(n_out * (k // 32) * 18)
             hip.synth_q4(wbuf, 1, n_out, k, args.seed, 1000 + len(mats))
-            mats[name] = (wbuf, hip.DevBuf.from_array(rng.standard_normal(k).astype(np.float32)),
-                          hip.DevBuf(n_out * 4), n_out, k)
+            xb = xin["ffn"] if name in ("ffn_gate", "ffn_up") else xin[k]
+            mats[name] = (wbuf, xb, hip.DevBuf(n_out * 4), n_out, k)
         hip.sync()
         reps = 200
+        groups = [["attn_q", "attn_k", "attn_v"], ["attn_output"], ["ffn_gate", "ffn_up"], ["ffn_down"]]
 
-        def timed(names) -> float:
+        def call(names) -> None:
+            if len(names) == 1:
+                wb, xb, yb, n_out, k = mats[names[0]]
+                hip.q4_mm(wb, xb, yb, n_out, k, 1)
+            else:  # one launch for the projections that share an input (rvm_q4_mm_n)
+                ms_ = [mats[nm] for nm in names]
+                hip.q4_mm_n([m[0] for m in ms_], ms_[0][1], [m[2] for m in ms_], [m[3] for m in ms_], ms_[0][4], 1)
+
+        def timed(names, fused: bool = False) -> float:
             hip.Graph.begin()
             for _ in range(reps):
                 for nm in names:
-                    wb, xb, yb, n_out, k = mats[nm]
-                    hip.q4_mm(wb, xb, yb, n_out, k, 1)
+                    if fused:
+                        call(nm)
+                    else:
+                        wb, xb, yb, n_out, k = mats[nm]
+                        hip.q4_mm(wb, xb, yb, n_out, k, 1)
             g = hip.Graph.end()
             g.launch()
             hip.sync()
@@ -314,9 +330,14 @@ def other_workload(args) -> int:
             per[name] = {"rows": n_out, "k": k, "us": round(ms1 * 1e3, 3),
                          "gb_s": round(n_out * (k // 32) * 18 / (ms1 / 1e3) / 1e9, 1)}
         layer_names = [nm for nm, _, _ in shapes]
-        ms = timed(layer_names)
+        ms_sep = timed(layer_names)
+        ms = timed(groups, fused=True)
         nbytes = sum(n_out * (k // 32) * 18 for _, n_out, k in shapes)
         achieved = nbytes / (ms / 1e3) / 1e9
+        per["layer_separate_calls"] = {"launches": 7, "us": round(ms_sep * 1e3, 3),
+                                       "gb_s": round(nbytes / (ms_sep / 1e3) / 1e9, 1)}
+        per["layer_shared_input_calls"] = {"launches": 4, "us": round(ms * 1e3, 3),
+                                           "entry": "rvm_q4_mm_n for q/k/v and gate/up, rvh_q4_mm for the others"}
         line.update({"metric": "dense Q4_0 GEMV GB/s, one layer's projections, batch 1", "value": round(achieved, 1),
                      "unit": "GB/s", "steps": reps, "warmup": reps, "ms_per_step": round(ms, 6),
                      "dtype": "int4 weights x f32 activations -> f32",

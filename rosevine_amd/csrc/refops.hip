@@ -58,8 +58,8 @@ __global__ __launch_bounds__(256) void k_f32_mm(const float *__restrict__ w, con
 
 // Q4_0 rows in the reference layout (18-byte blocks: f16 d, 16 nibble bytes; runtime/src/ops.rs:83-92)
 // times f32 activations, the dense GEMV/GEMM family behind rvh_q4_mm (runtime/hip/rvhip.hip; the
-// reference's k_q4_mm). Wave w takes rows QRW w .. QRW w + QRW-1 (1 to 8, so that there are about
-// 2048 waves) and lane l block columns l, l + 64, ...: each row's blocks are read as
+// reference's k_q4_mm). Workgroup (one wave) w takes rows QRW w .. QRW w + QRW-1 (1 to 8, so that
+// there are about 2048 waves) and lane l block columns l, l + 64, ...: each row's blocks are read as
 // one contiguous run per wave (a 16-byte nibble load per lane, at the block's 2-byte alignment), and
 // a lane's activation block is loaded once for the wave's rows.
 // A block adds d * (sum_j n_j x_j - 8 sum_j x_j) with n_j the unsigned nibbles (one byte convert
@@ -72,10 +72,13 @@ struct __attribute__((packed, aligned(2))) Q4Nibbles {
     uint32_t q[4];
 };
 
+// The rows of workgroup bx (one wave) of one matrix (blockIdx.y picks the tokens). One-wave
+// workgroups spread the rows over the CUs within a wave's rows of each other: with four waves per
+// workgroup, 2112 rows made 528 workgroups, three on some CUs and two on most (a third slower).
 template <int NCOL, int QRW, int TT>  // ceil(nb / 64) block columns per lane; rows per wave; tokens
-__global__ __launch_bounds__(256) void k_q4_mm(const uint8_t *__restrict__ w, const float *__restrict__ x,
-                                               float *__restrict__ y, int n_out, int k, int n_in) {
-    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * QRW, lane = threadIdx.x & 63;
+__device__ __forceinline__ void q4_mm_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
+                                           float *__restrict__ y, int n_out, int k, int n_in, int bx) {
+    const int r0 = bx * QRW, lane = threadIdx.x & 63;
     if (r0 >= n_out) return;
     const int t0 = blockIdx.y * TT, nt = min(TT, n_in - t0);
     const int nb = k / QK;
@@ -152,6 +155,32 @@ __global__ __launch_bounds__(256) void k_q4_mm(const uint8_t *__restrict__ w, co
     }
 }
 
+template <int NCOL, int QRW, int TT>
+__global__ __launch_bounds__(64) void k_q4_mm(const uint8_t *__restrict__ w, const float *__restrict__ x,
+                                              float *__restrict__ y, int n_out, int k, int n_in) {
+    q4_mm_rows<NCOL, QRW, TT>(w, x, y, n_out, k, n_in, blockIdx.x);
+}
+
+// Up to four matrices on one input in one launch: workgroups start[m] .. start[m + 1] - 1 take
+// matrix m, each row as k_q4_mm computes it (the same bits as one rvh_q4_mm call per matrix).
+constexpr int Q4_NMAT = 4;
+struct Q4Mats {
+    const uint8_t *w[Q4_NMAT];
+    float *y[Q4_NMAT];
+    int n_out[Q4_NMAT];
+    int start[Q4_NMAT];
+    int n;
+};
+
+template <int NCOL, int QRW, int TT>
+__global__ __launch_bounds__(64) void k_q4_mm_n(Q4Mats mats, const float *__restrict__ x, int k, int n_in) {
+    int m = 0;
+#pragma unroll
+    for (int i = 1; i < Q4_NMAT; ++i)
+        if (i < mats.n && (int)blockIdx.x >= mats.start[i]) m = i;
+    q4_mm_rows<NCOL, QRW, TT>(mats.w[m], x, mats.y[m], mats.n_out[m], k, n_in, blockIdx.x - mats.start[m]);
+}
+
 __global__ void k_geglu_split(const float *__restrict__ gu, float *__restrict__ out, size_t n, int ff) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -183,6 +212,39 @@ __global__ void k_moe_combine(const float *__restrict__ y, const int32_t *__rest
     }
 }
 
+// rows per wave for n_out rows in all: about 2048 waves, each with as many rows' bytes in flight as
+// that allows
+inline int q4_rows_per_wave(long n_out) { return n_out >= 16384 ? 8 : (n_out >= 8192 ? 4 : (n_out >= 4096 ? 2 : 1)); }
+
+// Calls go(kernel template instance) with the instance for (k, rows per wave rw, n_in).
+template <template <int, int, int> class K, typename Go>
+void q4_dispatch(int k, int rw, int n_in, Go &&go) {
+    const int ncol = min(grid_blocks(k / QK, 64), 4);
+    auto by_cols = [&](auto rwc, auto ttc) {
+        constexpr int RW = decltype(rwc)::value, T = decltype(ttc)::value;
+        if (ncol == 1) go(K<1, RW, T>::fn);
+        else if (ncol == 2) go(K<2, RW, T>::fn);
+        else if (ncol == 3) go(K<3, RW, T>::fn);
+        else go(K<4, RW, T>::fn);
+    };
+    auto by_rows = [&](auto ttc) {
+        if (rw == 8) by_cols(std::integral_constant<int, 8>{}, ttc);
+        else if (rw == 4) by_cols(std::integral_constant<int, 4>{}, ttc);
+        else if (rw == 2) by_cols(std::integral_constant<int, 2>{}, ttc);
+        else by_cols(std::integral_constant<int, 1>{}, ttc);
+    };
+    if (n_in == 1) by_rows(std::integral_constant<int, 1>{});
+    else by_rows(std::integral_constant<int, QTT>{});
+}
+template <int C, int R, int T>
+struct Q4One {
+    static constexpr auto fn = k_q4_mm<C, R, T>;
+};
+template <int C, int R, int T>
+struct Q4Many {
+    static constexpr auto fn = k_q4_mm_n<C, R, T>;
+};
+
 }  // namespace rvm
 
 using namespace rvm;
@@ -204,29 +266,38 @@ int rvh_f32_mm(const float *w, const float *x, float *y, int n_out, int k, int n
 int rvh_q4_mm(const void *w, const float *x, float *y, int n_out, int k, int n_in) {
     RVM_CHECK(w && x && y && n_out > 0 && n_in > 0 && k > 0 && k % QK == 0 && ((uintptr_t)w & 1) == 0);
     RVM_CHECK(grid_blocks(n_in, QTT) <= 65535);
-    // rows per wave: about 2048 waves, each with as many rows' bytes in flight as that allows
-    const int ncol = min(grid_blocks(k / QK, 64), 4);
-    const int rw = n_out >= 16384 ? 8 : (n_out >= 8192 ? 4 : (n_out >= 4096 ? 2 : 1));
-    const int tt = n_in == 1 ? 1 : QTT;
-    const dim3 grid(grid_blocks(n_out, 4 * rw), grid_blocks(n_in, tt));
-    auto go = [&](auto kern) {
-        hipLaunchKernelGGL(kern, grid, dim3(256), 0, cur_stream(), (const uint8_t *)w, x, y, n_out, k, n_in);
-    };
-    auto by_cols = [&](auto rwc, auto ttc) {
-        constexpr int RW = decltype(rwc)::value, T = decltype(ttc)::value;
-        if (ncol == 1) go(k_q4_mm<1, RW, T>);
-        else if (ncol == 2) go(k_q4_mm<2, RW, T>);
-        else if (ncol == 3) go(k_q4_mm<3, RW, T>);
-        else go(k_q4_mm<4, RW, T>);
-    };
-    auto by_rows = [&](auto ttc) {
-        if (rw == 8) by_cols(std::integral_constant<int, 8>{}, ttc);
-        else if (rw == 4) by_cols(std::integral_constant<int, 4>{}, ttc);
-        else if (rw == 2) by_cols(std::integral_constant<int, 2>{}, ttc);
-        else by_cols(std::integral_constant<int, 1>{}, ttc);
-    };
-    if (tt == 1) by_rows(std::integral_constant<int, 1>{});
-    else by_rows(std::integral_constant<int, QTT>{});
+    const int rw = q4_rows_per_wave(n_out);
+    const dim3 grid(grid_blocks(n_out, rw), grid_blocks(n_in, n_in == 1 ? 1 : QTT));
+    q4_dispatch<Q4One>(k, rw, n_in, [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(64), 0, cur_stream(), (const uint8_t *)w, x, y, n_out, k, n_in);
+    });
+    return launched();
+}
+
+int rvm_q4_mm_n(int n_mat, const void *const *w, const int *n_out, float *const *y, const float *x, int k, int n_in) {
+    RVM_CHECK(n_mat >= 1 && n_mat <= Q4_NMAT && w && n_out && y && x && n_in > 0 && k > 0 && k % QK == 0);
+    RVM_CHECK(grid_blocks(n_in, QTT) <= 65535);
+    long rows = 0;
+    for (int m = 0; m < n_mat; ++m) {
+        RVM_CHECK(w[m] && y[m] && n_out[m] > 0 && ((uintptr_t)w[m] & 1) == 0);
+        rows += n_out[m];
+    }
+    const int rw = q4_rows_per_wave(rows);
+    Q4Mats mats{};
+    long blocks = 0;
+    for (int m = 0; m < n_mat; ++m) {
+        mats.w[m] = (const uint8_t *)w[m];
+        mats.y[m] = y[m];
+        mats.n_out[m] = n_out[m];
+        mats.start[m] = (int)blocks;
+        blocks += grid_blocks(n_out[m], rw);
+    }
+    RVM_CHECK(blocks <= 0x7fffffffL);
+    mats.n = n_mat;
+    const dim3 grid((unsigned)blocks, grid_blocks(n_in, n_in == 1 ? 1 : QTT));
+    q4_dispatch<Q4Many>(k, rw, n_in, [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(64), 0, cur_stream(), mats, x, k, n_in);
+    });
     return launched();
 }
 

@@ -91,6 +91,7 @@ SIGNATURES = {
     "rvh_f32_mm": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "rvh_q4_mm": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "rvh_q4_mv": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "rvm_q4_mm_n": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i]),
     "rvh_geglu_split": (_i, [_vp, _vp, _i, _i]),
     "rvh_gather_rows": (_i, [_vp, _vp, _vp, _i, _i]),
     "rvh_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
@@ -398,6 +399,17 @@ def f32_mm(w: DevBuf, x: DevBuf, y: DevBuf, n_out: int, k: int, n_in: int) -> No
 def q4_mm(w: DevBuf, x: DevBuf, y: DevBuf, n_out: int, k: int, n_in: int) -> None:
     check(lib().rvh_q4_mm(_need(w, n_out * (k // QK) * Q4_BLOCK), _need(x, n_in * k * 4),
                           _need(y, n_in * n_out * 4), n_out, k, n_in))
+
+
+def q4_mm_n(ws: list, x: DevBuf, ys: list, n_outs: list, k: int, n_in: int) -> None:
+    """rvm_q4_mm_n: up to four rvh_q4_mm products on one input in one launch."""
+    n = len(ws)
+    if not (len(ys) == n and len(n_outs) == n):
+        raise ValueError("one output and one row count per matrix")
+    wp = (C.c_void_p * max(n, 1))(*[_need(w, r * (k // QK) * Q4_BLOCK) for w, r in zip(ws, n_outs)])
+    yp = (C.c_void_p * max(n, 1))(*[_need(y, n_in * r * 4) for y, r in zip(ys, n_outs)])
+    rp = (C.c_int * max(n, 1))(*n_outs)
+    check(lib().rvm_q4_mm_n(n, wp, rp, yp, _need(x, n_in * k * 4), k, n_in))
 
 
 def q4_mv(w: DevBuf, x: DevBuf, y: DevBuf, n_out: int, k: int, n_in: int) -> None:

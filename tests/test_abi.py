@@ -90,3 +90,17 @@ def test_phase_trace_only_in_the_diagnostic_build(rvlib):
     assert rvlib.rvm_phase_trace(buf.ctypes.data, buf.nbytes - 8) != 0
     assert rvlib.rvm_phase_trace(buf.ctypes.data, buf.nbytes) == 801  # hipErrorNotSupported
     assert not buf.any()
+
+
+def test_q4_mm_n_rejects_bad_counts_before_any_call(rvlib):
+    """rvm_q4_mm_n validates its matrix count and arrays on the host (no device call is made)."""
+    import ctypes as C
+    w = (C.c_void_p * 5)(*([0x1000] * 5))
+    y = (C.c_void_p * 5)(*([0x2000] * 5))
+    rows = (C.c_int * 5)(*([64] * 5))
+    for n in (0, 5):
+        assert rvlib.rvm_q4_mm_n(n, w, rows, y, C.c_void_p(0x3000), 2816, 1) == 1  # hipErrorInvalidValue
+    odd = (C.c_void_p * 2)(0x1000, 0x1001)  # a matrix that is not 2-byte aligned
+    assert rvlib.rvm_q4_mm_n(2, odd, rows, y, C.c_void_p(0x3000), 2816, 1) == 1
+    bad_rows = (C.c_int * 2)(64, 0)
+    assert rvlib.rvm_q4_mm_n(2, w, bad_rows, y, C.c_void_p(0x3000), 2816, 1) == 1

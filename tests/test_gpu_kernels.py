@@ -249,3 +249,25 @@ def test_out_of_range_calls_are_refused(gpu):
     with pytest.raises(hip.DeviceError) as e:
         hip.check(hip.lib().rvm_q4q8_mm(small.ptr, 9, small.ptr, small.ptr, 64, 64, 1))
     assert e.value.code == 1
+
+
+@pytest.mark.parametrize("rows,k", [
+    ((4096, 2048, 2048), 2816),   # q, k, v of a sliding-window layer (contract.rs:41-62)
+    ((2112, 2112), 2816),         # gate and up
+    ((5, 33, 64, 130), 96),       # four matrices, row counts that split workgroups, a short k
+    ((1000,), 4096),              # one matrix
+])
+def test_q4_mm_n_equals_one_call_per_matrix(gpu, rows, k):
+    """rvm_q4_mm_n: each matrix's output is rvh_q4_mm's, bit for bit, for one and for three tokens."""
+    rng = np.random.default_rng(sum(rows) + k)
+    ws = [hip.DevBuf(r * (k // 32) * 18) for r in rows]
+    for i, (w, r) in enumerate(zip(ws, rows)):
+        hip.synth_q4(w, 1, r, k, 7, 50 + i)
+    for n_in in (1, 3):
+        x = dev((rng.standard_normal((n_in, k)) * 0.5).astype(np.float32))
+        ys = [hip.DevBuf(n_in * r * 4) for r in rows]
+        hip.q4_mm_n(ws, x, ys, list(rows), k, n_in)
+        for w, y, r in zip(ws, ys, rows):
+            y1 = hip.DevBuf(n_in * r * 4)
+            hip.q4_mm(w, x, y1, r, k, n_in)
+            assert np.array_equal(y.download(np.float32, n_in * r), y1.download(np.float32, n_in * r)), (rows, r, n_in)
