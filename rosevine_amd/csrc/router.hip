@@ -290,31 +290,44 @@ __device__ __forceinline__ float4 buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_
     return f;
 }
 
-// Quad M of a 64-column row block: columns 4M .. 4M+3 sit in lane M of each row of 16 lanes
-// (w.x .. w.w). Each is handed to every lane by a DPP row broadcast inside the multiply
+// Quads MA and MB of a 64-column row block: columns 4M .. 4M+3 sit in lane M of each row of 16
+// lanes (w.x .. w.w). Each is handed to every lane by a DPP row broadcast inside the multiply
 // (v_mul_f32_dpp row_newbcast: the plain f32 product, rounded) and added to this lane's fold in
-// column order. Written out because the compiler keeps the broadcast as a separate move (its unused
-// old operand comes from another block), and as one statement per quad because the compiler puts a
-// wait state in front of every statement that holds a DPP instruction. The hardware needs two wait
-// states between a VALU write of a DPP source and its read: every w here comes from an LDS read.
-template <int M>
-__device__ __forceinline__ void fold_quad(float &acc, const float4 &w, const float4 &v) {
-    float p;
-    asm("v_mul_f32_dpp %1, %2, %6 row_newbcast:%10 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+// column order. The products are formed ahead of the adds that take them (quad MA's four first,
+// quad MB's between quad MA's adds), so each add waits only for the add before it: the fold is the
+// chain of dependent adds, and a product made just before its add put a multiply's latency on that
+// chain for every column. Written out because the compiler keeps the broadcast as a separate move
+// (its unused old operand comes from another block) and puts a wait state in front of every
+// statement that holds a DPP instruction. The hardware needs two wait states between a VALU write
+// of a DPP source and its read: every w here comes from an LDS read.
+template <int MA, int MB>
+__device__ __forceinline__ void fold_quad2(float &acc, const float4 &w, const float4 &a, const float4 &b) {
+    float t0, t1, t2, t3, t4, t5, t6, t7;
+    asm("v_mul_f32_dpp %1, %9, %13 row_newbcast:%21 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_mul_f32_dpp %2, %10, %14 row_newbcast:%21 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_mul_f32_dpp %3, %11, %15 row_newbcast:%21 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_mul_f32_dpp %4, %12, %16 row_newbcast:%21 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
         "v_add_f32 %0, %0, %1\n\t"
-        "v_mul_f32_dpp %1, %3, %7 row_newbcast:%10 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
-        "v_add_f32 %0, %0, %1\n\t"
-        "v_mul_f32_dpp %1, %4, %8 row_newbcast:%10 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
-        "v_add_f32 %0, %0, %1\n\t"
-        "v_mul_f32_dpp %1, %5, %9 row_newbcast:%10 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
-        "v_add_f32 %0, %0, %1"
-        : "+v"(acc), "=&v"(p)
-        : "v"(w.x), "v"(w.y), "v"(w.z), "v"(w.w), "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w), "i"(M));
+        "v_mul_f32_dpp %5, %9, %17 row_newbcast:%22 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32 %0, %0, %2\n\t"
+        "v_mul_f32_dpp %6, %10, %18 row_newbcast:%22 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32 %0, %0, %3\n\t"
+        "v_mul_f32_dpp %7, %11, %19 row_newbcast:%22 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32 %0, %0, %4\n\t"
+        "v_mul_f32_dpp %8, %12, %20 row_newbcast:%22 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32 %0, %0, %5\n\t"
+        "v_add_f32 %0, %0, %6\n\t"
+        "v_add_f32 %0, %0, %7\n\t"
+        "v_add_f32 %0, %0, %8"
+        : "+v"(acc), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3), "=&v"(t4), "=&v"(t5), "=&v"(t6), "=&v"(t7)
+        : "v"(w.x), "v"(w.y), "v"(w.z), "v"(w.w), "v"(a.x), "v"(a.y), "v"(a.z), "v"(a.w), "v"(b.x), "v"(b.y),
+          "v"(b.z), "v"(b.w), "i"(MA), "i"(MB));
 }
 template <int BASE, int... Q>
 __device__ __forceinline__ void fold_quads(float &acc, const float4 &w, const float4 *xv,
                                            std::integer_sequence<int, Q...>) {
-    (fold_quad<BASE + Q>(acc, w, xv[Q]), ...);  // left to right: the quads in column order
+    // left to right: the quad pairs in column order
+    (fold_quad2<BASE + 2 * Q, BASE + 2 * Q + 1>(acc, w, xv[2 * Q], xv[2 * Q + 1]), ...);
 }
 
 template <int F4>
@@ -396,7 +409,7 @@ __global__ __launch_bounds__(FW * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
                     const int qq = (r + 1) * SQ + q;
                     xv[(r + 1) & 1][q] = xs[buf][qq][lane ^ (qq & 7)];
                 }
-            fold_quads<(r & 1) * SQ>(acc, wb[r >> 1], xv[r & 1], std::make_integer_sequence<int, SQ>{});
+            fold_quads<(r & 1) * SQ>(acc, wb[r >> 1], xv[r & 1], std::make_integer_sequence<int, SQ / 2>{});
             __builtin_amdgcn_sched_barrier(0);
         };
         sub(std::integral_constant<int, 0>{});
