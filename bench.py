@@ -435,7 +435,7 @@ def other_workload(args) -> int:
         line.update({"metric": "decode attention (attn_core: KV store + split-K attention), 30 layers, depth 16384, "
                                "batch 1: per-token time and K+V GB/s",
                      "value": round(achieved, 1), "unit": "GB/s", "higher_is_better": True, "steps": reps,
-                     "warmup": reps, "ms_per_step": round(ms, 6), "dtype": "Q8_0 K/V x f32 q -> f32 (bf16x3 MFMA scores)",
+                     "warmup": reps, "ms_per_step": round(ms, 6), "dtype": "Q8_0 K/V x f32 q -> f32 (bf16x3 MFMA scores and values)",
                      "data": "synthetic (random Q8_0 rings, N(0,0.2) queries)", "scaling": "weak",
                      "config": {"workload": "attn", "depth": depth, "layers": per,
                                 "chunk_policy": f"runtime/src/hip.rs:486-490 with target {target} (the reference's 1024) "
