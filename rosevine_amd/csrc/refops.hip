@@ -59,87 +59,103 @@ __global__ __launch_bounds__(256) void k_f32_mm(const float *__restrict__ w, con
 // Q4_0 rows in the reference layout (18-byte blocks: f16 d, 16 nibble bytes; runtime/src/ops.rs:83-92)
 // times f32 activations, the dense GEMV/GEMM family behind rvh_q4_mm (runtime/hip/rvhip.hip; the
 // reference's k_q4_mm). Workgroup (one wave) w takes rows QRW w .. QRW w + QRW-1 (1 to 8, so that
-// there are about 2048 waves) and lane l block columns l, l + 64, ...: each row's blocks are read as
-// one contiguous run per wave (a 16-byte nibble load per lane, at the block's 2-byte alignment), and
-// a lane's activation block is loaded once for the wave's rows.
-// A block adds d * (sum_j n_j x_j - 8 sum_j x_j) with n_j the unsigned nibbles (one byte convert
+// there are about 2048 waves) and lane l item columns l, l + 64, ... (an item is a block or half of
+// one): each row's items are read as one contiguous run per wave (a 16- or 8-byte nibble load per
+// lane, at the block's 2-byte alignment), and a lane's activations are loaded once for the wave's rows.
+// An item adds d * (sum_j n_j x_j - 8 sum_j x_j) with n_j its unsigned nibbles (one byte convert
 // and one fused multiply-add per element), which is sum_j ((n_j - 8) d) x_j up to rounding; the
 // reference's CPU ops are the tolerance target (runtime/tests/hip_ops.rs:56-81). Each output is
-// summed in a fixed order (blocks per lane in column order, then a fixed wave reduction), so a
+// summed in a fixed order (items per lane in column order, then a fixed wave reduction), so a
 // token's result does not depend on the other tokens of the call.
 constexpr int QTT = 8;  // tokens per pass (calls with one token use a one-token variant)
+template <int NW>
 struct __attribute__((packed, aligned(2))) Q4Nibbles {
-    uint32_t q[4];
+    uint32_t q[NW];
 };
 
+// An item is a whole block (SUB 1) or half of one (SUB 2: nibble bytes 8h .. 8h+7, elements
+// 8h .. 8h+7 and 16+8h .. 16+8h+7, with the block's d). Half blocks keep more lanes busy where a
+// row's blocks leave the last column of lanes mostly idle: 88 blocks of a 2816-wide row fill 2 x 64
+// lanes to 69%, its 176 halves fill 3 x 64 lanes to 92% at half the work per item.
 // The rows of workgroup bx (one wave) of one matrix (blockIdx.y picks the tokens). One-wave
 // workgroups spread the rows over the CUs within a wave's rows of each other: with four waves per
 // workgroup, 2112 rows made 528 workgroups, three on some CUs and two on most (a third slower).
-template <int NCOL, int QRW, int TT>  // ceil(nb / 64) block columns per lane; rows per wave; tokens
+template <int SUB, int NCOL, int QRW, int TT>  // items per block; item columns per lane; rows per wave; tokens
 __device__ __forceinline__ void q4_mm_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
                                            float *__restrict__ y, int n_out, int k, int n_in, int bx) {
+    constexpr int NW = 4 / SUB, NB = 4 * NW, NE = 2 * NB;  // nibble dwords, bytes and elements per item
     const int r0 = bx * QRW, lane = threadIdx.x & 63;
     if (r0 >= n_out) return;
     const int t0 = blockIdx.y * TT, nt = min(TT, n_in - t0);
-    const int nb = k / QK;
+    const int nb = k / QK, ni = nb * SUB;
     const size_t rb = (size_t)nb * Q4_BLOCK;
     float acc[QRW][TT];
 #pragma unroll
     for (int r = 0; r < QRW; ++r)
 #pragma unroll
         for (int t = 0; t < TT; ++t) acc[r][t] = 0.0f;
-    for (int cg = 0; cg < nb; cg += 64 * NCOL) {  // one pass unless k > 64 NCOL blocks
+    for (int cg = 0; cg < ni; cg += 64 * NCOL) {  // one pass unless a row has more than 64 NCOL items
         // the group's weight loads first: QRW rows x NCOL columns (rows and columns past the end clamped)
         float d[NCOL][QRW];
-        uint32_t q[NCOL][QRW][4];
+        uint32_t q[NCOL][QRW][NW];
+        uint32_t xo[NCOL];  // the item's first activation within a token's row
 #pragma unroll
-        for (int c = 0; c < NCOL; ++c)
+        for (int c = 0; c < NCOL; ++c) {
+            const uint32_t it = min(cg + lane + 64 * c, ni - 1), bo = it / SUB * Q4_BLOCK;
+            const uint32_t qo = bo + 2 + it % SUB * NB;
+            xo[c] = it / SUB * QK + it % SUB * NB;
 #pragma unroll
             for (int r = 0; r < QRW; ++r) {
-                const uint8_t *blk =
-                    w + (size_t)min(r0 + r, n_out - 1) * rb + (size_t)min(cg + lane + 64 * c, nb - 1) * Q4_BLOCK;
-                d[c][r] = h2f(*(const uint16_t *)blk);
-                const Q4Nibbles v = *(const Q4Nibbles *)(blk + 2);
+                // the row's start is the same for the whole wave; lanes add a 32-bit offset
+                const uint8_t *row = w + (size_t)__builtin_amdgcn_readfirstlane(min(r0 + r, n_out - 1)) * rb;
+                d[c][r] = h2f(*(const uint16_t *)(row + bo));
+                const Q4Nibbles<NW> v = *(const Q4Nibbles<NW> *)(row + qo);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) q[c][r][j] = v.q[j];
+                for (int j = 0; j < NW; ++j) q[c][r][j] = v.q[j];
             }
+        }
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
             if (t >= nt) break;
+            const float *xt = x + (size_t)(t0 + t) * k;
 #pragma unroll
             for (int c = 0; c < NCOL; ++c) {
-                const int b = cg + lane + 64 * c;
-                if (b >= nb) break;
-                const float4 *xb = (const float4 *)(x + (size_t)(t0 + t) * k + (size_t)b * QK);
-                float xv[QK];
+                if (cg + lane + 64 * c >= ni) break;
+                const float *xb = xt + xo[c];
+                float xv[NE];  // the item's low-nibble elements, then its high-nibble ones
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float4 v = xb[i];
-                    xv[4 * i] = v.x;
-                    xv[4 * i + 1] = v.y;
-                    xv[4 * i + 2] = v.z;
-                    xv[4 * i + 3] = v.w;
+                for (int i = 0; i < NB / 4; ++i) {
+                    const float4 lo = ((const float4 *)xb)[i], hi = ((const float4 *)(xb + 16))[i];
+                    xv[4 * i] = lo.x;
+                    xv[4 * i + 1] = lo.y;
+                    xv[4 * i + 2] = lo.z;
+                    xv[4 * i + 3] = lo.w;
+                    xv[NB + 4 * i] = hi.x;
+                    xv[NB + 4 * i + 1] = hi.y;
+                    xv[NB + 4 * i + 2] = hi.z;
+                    xv[NB + 4 * i + 3] = hi.w;
                 }
                 float xs = 0.0f;
 #pragma unroll
-                for (int i = 0; i < QK; ++i) xs += xv[i];
+                for (int i = 0; i < NE; ++i) xs += xv[i];
 #pragma unroll
                 for (int r = 0; r < QRW; ++r) {
-                    float s = 0.0f;
+                    // low nibbles as they lie, high nibbles in place (16 n, scaled back once)
+                    float sl = 0.0f, sh = 0.0f;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
+                    for (int j = 0; j < NW; ++j) {
                         const uint32_t lo = and_opaque(q[c][r][j], 0x0F0F0F0Fu);
-                        const uint32_t hi = and_opaque(q[c][r][j] >> 4, 0x0F0F0F0Fu);
-                        s = fmaf((float)(lo & 0xFF), xv[4 * j], s);
-                        s = fmaf((float)((lo >> 8) & 0xFF), xv[4 * j + 1], s);
-                        s = fmaf((float)((lo >> 16) & 0xFF), xv[4 * j + 2], s);
-                        s = fmaf((float)(lo >> 24), xv[4 * j + 3], s);
-                        s = fmaf((float)(hi & 0xFF), xv[16 + 4 * j], s);
-                        s = fmaf((float)((hi >> 8) & 0xFF), xv[16 + 4 * j + 1], s);
-                        s = fmaf((float)((hi >> 16) & 0xFF), xv[16 + 4 * j + 2], s);
-                        s = fmaf((float)(hi >> 24), xv[16 + 4 * j + 3], s);
+                        const uint32_t hi = and_opaque(q[c][r][j], 0xF0F0F0F0u);
+                        sl = fmaf((float)(lo & 0xFF), xv[4 * j], sl);
+                        sh = fmaf((float)(hi & 0xFF), xv[NB + 4 * j], sh);
+                        sl = fmaf((float)((lo >> 8) & 0xFF), xv[4 * j + 1], sl);
+                        sh = fmaf((float)((hi >> 8) & 0xFF), xv[NB + 4 * j + 1], sh);
+                        sl = fmaf((float)((lo >> 16) & 0xFF), xv[4 * j + 2], sl);
+                        sh = fmaf((float)((hi >> 16) & 0xFF), xv[NB + 4 * j + 2], sh);
+                        sl = fmaf((float)(lo >> 24), xv[4 * j + 3], sl);
+                        sh = fmaf((float)(hi >> 24), xv[NB + 4 * j + 3], sh);
                     }
-                    acc[r][t] = fmaf(d[c][r], s - 8.0f * xs, acc[r][t]);
+                    acc[r][t] = fmaf(d[c][r], fmaf(sh, 0.0625f, sl) - 8.0f * xs, acc[r][t]);
                 }
             }
         }
@@ -155,10 +171,10 @@ __device__ __forceinline__ void q4_mm_rows(const uint8_t *__restrict__ w, const 
     }
 }
 
-template <int NCOL, int QRW, int TT>
+template <int SUB, int NCOL, int QRW, int TT>
 __global__ __launch_bounds__(64) void k_q4_mm(const uint8_t *__restrict__ w, const float *__restrict__ x,
                                               float *__restrict__ y, int n_out, int k, int n_in) {
-    q4_mm_rows<NCOL, QRW, TT>(w, x, y, n_out, k, n_in, blockIdx.x);
+    q4_mm_rows<SUB, NCOL, QRW, TT>(w, x, y, n_out, k, n_in, blockIdx.x);
 }
 
 // Up to four matrices on one input in one launch: workgroups start[m] .. start[m + 1] - 1 take
@@ -172,13 +188,13 @@ struct Q4Mats {
     int n;
 };
 
-template <int NCOL, int QRW, int TT>
+template <int SUB, int NCOL, int QRW, int TT>
 __global__ __launch_bounds__(64) void k_q4_mm_n(Q4Mats mats, const float *__restrict__ x, int k, int n_in) {
     int m = 0;
 #pragma unroll
     for (int i = 1; i < Q4_NMAT; ++i)
         if (i < mats.n && (int)blockIdx.x >= mats.start[i]) m = i;
-    q4_mm_rows<NCOL, QRW, TT>(mats.w[m], x, mats.y[m], mats.n_out[m], k, n_in, blockIdx.x - mats.start[m]);
+    q4_mm_rows<SUB, NCOL, QRW, TT>(mats.w[m], x, mats.y[m], mats.n_out[m], k, n_in, blockIdx.x - mats.start[m]);
 }
 
 __global__ void k_geglu_split(const float *__restrict__ gu, float *__restrict__ out, size_t n, int ff) {
@@ -216,16 +232,23 @@ __global__ void k_moe_combine(const float *__restrict__ y, const int32_t *__rest
 // that allows
 inline int q4_rows_per_wave(long n_out) { return n_out >= 16384 ? 8 : (n_out >= 8192 ? 4 : (n_out >= 4096 ? 2 : 1)); }
 
-// Calls go(kernel template instance) with the instance for (k, rows per wave rw, n_in).
-template <template <int, int, int> class K, typename Go>
+// Calls go(kernel template instance) with the instance for (k, rows per wave rw, n_in). Half-block
+// items where they take fewer lane passes than whole blocks: 1 .. 32 blocks (one column of halves
+// against one of blocks at twice the work) and 65 .. 96 (three columns of halves against two of
+// blocks). The choice depends on k alone, so every token of a batch sums in the same order.
+template <template <int, int, int, int> class K, typename Go>
 void q4_dispatch(int k, int rw, int n_in, Go &&go) {
-    const int ncol = min(grid_blocks(k / QK, 64), 4);
+    const int nb = k / QK, ncol = min(grid_blocks(nb, 64), 4);
+    const bool halves = nb <= 32 || (nb > 64 && nb <= 96);
     auto by_cols = [&](auto rwc, auto ttc) {
         constexpr int RW = decltype(rwc)::value, T = decltype(ttc)::value;
-        if (ncol == 1) go(K<1, RW, T>::fn);
-        else if (ncol == 2) go(K<2, RW, T>::fn);
-        else if (ncol == 3) go(K<3, RW, T>::fn);
-        else go(K<4, RW, T>::fn);
+        if (halves) {
+            if (nb <= 32) go(K<2, 1, RW, T>::fn);
+            else go(K<2, 3, RW, T>::fn);
+        } else if (ncol == 1) go(K<1, 1, RW, T>::fn);
+        else if (ncol == 2) go(K<1, 2, RW, T>::fn);
+        else if (ncol == 3) go(K<1, 3, RW, T>::fn);
+        else go(K<1, 4, RW, T>::fn);
     };
     auto by_rows = [&](auto ttc) {
         if (rw == 8) by_cols(std::integral_constant<int, 8>{}, ttc);
@@ -236,13 +259,13 @@ void q4_dispatch(int k, int rw, int n_in, Go &&go) {
     if (n_in == 1) by_rows(std::integral_constant<int, 1>{});
     else by_rows(std::integral_constant<int, QTT>{});
 }
-template <int C, int R, int T>
+template <int S, int C, int R, int T>
 struct Q4One {
-    static constexpr auto fn = k_q4_mm<C, R, T>;
+    static constexpr auto fn = k_q4_mm<S, C, R, T>;
 };
-template <int C, int R, int T>
+template <int S, int C, int R, int T>
 struct Q4Many {
-    static constexpr auto fn = k_q4_mm_n<C, R, T>;
+    static constexpr auto fn = k_q4_mm_n<S, C, R, T>;
 };
 
 }  // namespace rvm
