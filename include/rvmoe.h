@@ -56,8 +56,9 @@ int rvh_f32_mm(const float *w, const float *x, float *y, int n_out, int k, int n
 int rvh_q4_mm(const void *w, const float *x, float *y, int n_out, int k, int n_in);
 /* rvh_q4_mm's result up to summation order; x 16-byte aligned, w 2-byte aligned; rvhip.h:46-48. */
 int rvh_q4_mv(const void *w, const float *x, float *y, int n_out, int k, int n_in);
-/* n_mat (1 to 4) rvh_q4_mm products on one input in one launch: y[m] = w[m] x for matrices of
- * n_out[m] rows (each 2-byte aligned), the bits of rvh_q4_mm per matrix. w, n_out and y are host
+/* n_mat (1 to 4) rvh_q4_mm products on one input in one launch (matrices of 16384 rows or more,
+ * k <= 8192, take a launch each): y[m] = w[m] x for matrices of n_out[m] rows (each 2-byte
+ * aligned), the bits of rvh_q4_mm per matrix. w, n_out and y are host
  * arrays. No counterpart in rvhip.h: the reference runs one rvh_q4_mm per projection on the same
  * input (q, k, v: runtime/src/hip_exec.rs:728-731; gate, up: :773-774). */
 int rvm_q4_mm_n(int n_mat, const void *const *w, const int *n_out, float *const *y, const float *x, int k, int n_in);

@@ -72,38 +72,61 @@ template <int NW>
 struct __attribute__((packed, aligned(2))) Q4Nibbles {
     uint32_t q[NW];
 };
+template <int N>
+struct __attribute__((packed, aligned(4))) Dwords {
+    uint32_t q[N];
+};
 
 // An item is a whole block (SUB 1) or half of one (SUB 2: nibble bytes 8h .. 8h+7, elements
 // 8h .. 8h+7 and 16+8h .. 16+8h+7, with the block's d). Half blocks keep more lanes busy where a
 // row's blocks leave the last column of lanes mostly idle: 88 blocks of a 2816-wide row fill 2 x 64
 // lanes to 69%, its 176 halves fill 3 x 64 lanes to 92% at half the work per item.
-// The rows of workgroup bx (one wave) of one matrix (blockIdx.y picks the tokens). One-wave
-// workgroups spread the rows over the CUs within a wave's rows of each other: with four waves per
-// workgroup, 2112 rows made 528 workgroups, three on some CUs and two on most (a third slower).
-template <int SUB, int NCOL, int QRW, int TT>  // items per block; item columns per lane; rows per wave; tokens
-__device__ __forceinline__ void q4_mm_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
-                                           float *__restrict__ y, int n_out, int k, int n_in, int bx) {
-    constexpr int NW = 4 / SUB, NB = 4 * NW, NE = 2 * NB;  // nibble dwords, bytes and elements per item
-    const int r0 = bx * QRW, lane = threadIdx.x & 63;
-    if (r0 >= n_out) return;
-    const int t0 = blockIdx.y * TT, nt = min(TT, n_in - t0);
-    const int nb = k / QK, ni = nb * SUB;
-    const size_t rb = (size_t)nb * Q4_BLOCK;
-    float acc[QRW][TT];
+// Loads QRW rows from r0 x NCOL item columns from cg of one matrix (rows and columns past the end
+// clamped): each (item, row)'s d and nibble dwords, and each item's first activation within a row of x.
+template <int SUB, int NCOL, int QRW>
+__device__ __forceinline__ void q4_load_items(const uint8_t *__restrict__ w, size_t rb, int n_out, int r0, int cg,
+                                              int ni, bool aligned, float (&d)[NCOL][QRW],
+                                              uint32_t (&q)[NCOL][QRW][4 / SUB], uint32_t (&xo)[NCOL]) {
+    constexpr int NW = 4 / SUB, NB = 4 * NW;
+    const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int r = 0; r < QRW; ++r)
+    for (int c = 0; c < NCOL; ++c) {
+        const uint32_t it = min(cg + lane + 64 * c, ni - 1), b = it / SUB, h = it % SUB;
+        xo[c] = b * QK + h * NB;
+        if (aligned) {
+            // Dword-aligned loads that cover the item: a block starts on a dword (even b) or 2 bytes
+            // past one (odd b), so the load starts at 18 b + 8 h, 2 bytes earlier for odd b, and a
+            // byte permute picks the nibble dwords. Every load stays inside the matrix: an odd
+            // block's loads start 2 bytes into the block before it, an even block's whole-block
+            // load ends 2 bytes into the block after it, and a row's last block is odd.
+            const uint32_t odd = b & 1, a = b * Q4_BLOCK + h * 8 - 2 * odd;
+            const uint32_t sel = odd ? 0x07060504u : 0x05040302u;
 #pragma unroll
-        for (int t = 0; t < TT; ++t) acc[r][t] = 0.0f;
-    for (int cg = 0; cg < ni; cg += 64 * NCOL) {  // one pass unless a row has more than 64 NCOL items
-        // the group's weight loads first: QRW rows x NCOL columns (rows and columns past the end clamped)
-        float d[NCOL][QRW];
-        uint32_t q[NCOL][QRW][NW];
-        uint32_t xo[NCOL];  // the item's first activation within a token's row
+            for (int r = 0; r < QRW; ++r) {
+                const uint8_t *row = w + (size_t)__builtin_amdgcn_readfirstlane(min(r0 + r, n_out - 1)) * rb;
+                uint32_t v[NW + 1];
+                if constexpr (SUB == 2) {
+                    const Dwords<3> u = *(const Dwords<3> *)(row + a);
+                    v[0] = u.q[0];
+                    v[1] = u.q[1];
+                    v[2] = u.q[2];
+                } else {
+                    const Dwords<4> u = *(const Dwords<4> *)(row + a);
+                    v[0] = u.q[0];
+                    v[1] = u.q[1];
+                    v[2] = u.q[2];
+                    v[3] = u.q[3];
+                    v[4] = *(const uint32_t *)(row + a + 16);
+                }
 #pragma unroll
-        for (int c = 0; c < NCOL; ++c) {
-            const uint32_t it = min(cg + lane + 64 * c, ni - 1), bo = it / SUB * Q4_BLOCK;
-            const uint32_t qo = bo + 2 + it % SUB * NB;
-            xo[c] = it / SUB * QK + it % SUB * NB;
+                for (int j = 0; j < NW; ++j) q[c][r][j] = __builtin_amdgcn_perm(v[j + 1], v[j], sel);
+                uint32_t dbits = v[0] >> (16 * odd);
+                // the second half of a block takes d from the first half's lane (lane ^ 1)
+                if constexpr (SUB == 2) dbits = __builtin_amdgcn_mov_dpp(dbits, 0xA0, 0xF, 0xF, false);
+                d[c][r] = h2f((uint16_t)dbits);
+            }
+        } else {
+            const uint32_t bo = b * Q4_BLOCK, qo = bo + 2 + h * NB;
 #pragma unroll
             for (int r = 0; r < QRW; ++r) {
                 // the row's start is the same for the whole wave; lanes add a 32-bit offset
@@ -114,6 +137,83 @@ __device__ __forceinline__ void q4_mm_rows(const uint8_t *__restrict__ w, const 
                 for (int j = 0; j < NW; ++j) q[c][r][j] = v.q[j];
             }
         }
+    }
+}
+
+// An item's activations (its low-nibble elements, then its high-nibble ones); returns their sum.
+template <int SUB>
+__device__ __forceinline__ float q4_item_x(const float *__restrict__ xb, float (&xv)[32 / SUB]) {
+    constexpr int NB = 16 / SUB;
+#pragma unroll
+    for (int i = 0; i < NB / 4; ++i) {
+        const float4 lo = ((const float4 *)xb)[i], hi = ((const float4 *)(xb + 16))[i];
+        xv[4 * i] = lo.x;
+        xv[4 * i + 1] = lo.y;
+        xv[4 * i + 2] = lo.z;
+        xv[4 * i + 3] = lo.w;
+        xv[NB + 4 * i] = hi.x;
+        xv[NB + 4 * i + 1] = hi.y;
+        xv[NB + 4 * i + 2] = hi.z;
+        xv[NB + 4 * i + 3] = hi.w;
+    }
+    float xs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2 * NB; ++i) xs += xv[i];
+    return xs;
+}
+
+// acc + d (sum_j n_j x_j - 8 sum_j x_j) over one item: low nibbles as they lie, high nibbles in place
+// (16 n, scaled back once)
+template <int SUB>
+__device__ __forceinline__ float q4_item_dot(const uint32_t (&q)[4 / SUB], const float (&xv)[32 / SUB], float d,
+                                             float xs, float acc) {
+    constexpr int NW = 4 / SUB, NB = 4 * NW;
+    float sl = 0.0f, sh = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        const uint32_t lo = and_opaque(q[j], 0x0F0F0F0Fu);
+        const uint32_t hi = and_opaque(q[j], 0xF0F0F0F0u);
+        sl = fmaf((float)(lo & 0xFF), xv[4 * j], sl);
+        sh = fmaf((float)(hi & 0xFF), xv[NB + 4 * j], sh);
+        sl = fmaf((float)((lo >> 8) & 0xFF), xv[4 * j + 1], sl);
+        sh = fmaf((float)((hi >> 8) & 0xFF), xv[NB + 4 * j + 1], sh);
+        sl = fmaf((float)((lo >> 16) & 0xFF), xv[4 * j + 2], sl);
+        sh = fmaf((float)((hi >> 16) & 0xFF), xv[NB + 4 * j + 2], sh);
+        sl = fmaf((float)(lo >> 24), xv[4 * j + 3], sl);
+        sh = fmaf((float)(hi >> 24), xv[NB + 4 * j + 3], sh);
+    }
+    return fmaf(d, fmaf(sh, 0.0625f, sl) - 8.0f * xs, acc);
+}
+
+// rows of an even block count on a 4-byte aligned matrix: every row starts on a dword
+__host__ __device__ __forceinline__ bool q4_rows_aligned(const uint8_t *w, int nb) {
+    return (nb & 1) == 0 && ((uintptr_t)w & 3) == 0;
+}
+
+// The rows of workgroup bx (one wave) of one matrix (blockIdx.y picks the tokens). One-wave
+// workgroups spread the rows over the CUs within a wave's rows of each other: with four waves per
+// workgroup, 2112 rows made 528 workgroups, three on some CUs and two on most (a third slower).
+template <int SUB, int NCOL, int QRW, int TT>  // items per block; item columns per lane; rows per wave; tokens
+__device__ __forceinline__ void q4_mm_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
+                                           float *__restrict__ y, int n_out, int k, int n_in, int bx) {
+    constexpr int NW = 4 / SUB, NE = 32 / SUB;
+    const int r0 = bx * QRW, lane = threadIdx.x & 63;
+    if (r0 >= n_out) return;
+    const int t0 = blockIdx.y * TT, nt = min(TT, n_in - t0);
+    const int nb = k / QK, ni = nb * SUB;
+    const size_t rb = (size_t)nb * Q4_BLOCK;
+    const bool aligned = q4_rows_aligned(w, nb);
+    float acc[QRW][TT];
+#pragma unroll
+    for (int r = 0; r < QRW; ++r)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[r][t] = 0.0f;
+    for (int cg = 0; cg < ni; cg += 64 * NCOL) {  // one pass unless a row has more than 64 NCOL items
+        // the group's weight loads first
+        float d[NCOL][QRW];
+        uint32_t q[NCOL][QRW][NW];
+        uint32_t xo[NCOL];
+        q4_load_items<SUB, NCOL, QRW>(w, rb, n_out, r0, cg, ni, aligned, d, q, xo);
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
             if (t >= nt) break;
@@ -121,42 +221,10 @@ __device__ __forceinline__ void q4_mm_rows(const uint8_t *__restrict__ w, const 
 #pragma unroll
             for (int c = 0; c < NCOL; ++c) {
                 if (cg + lane + 64 * c >= ni) break;
-                const float *xb = xt + xo[c];
-                float xv[NE];  // the item's low-nibble elements, then its high-nibble ones
+                float xv[NE];
+                const float xs = q4_item_x<SUB>(xt + xo[c], xv);
 #pragma unroll
-                for (int i = 0; i < NB / 4; ++i) {
-                    const float4 lo = ((const float4 *)xb)[i], hi = ((const float4 *)(xb + 16))[i];
-                    xv[4 * i] = lo.x;
-                    xv[4 * i + 1] = lo.y;
-                    xv[4 * i + 2] = lo.z;
-                    xv[4 * i + 3] = lo.w;
-                    xv[NB + 4 * i] = hi.x;
-                    xv[NB + 4 * i + 1] = hi.y;
-                    xv[NB + 4 * i + 2] = hi.z;
-                    xv[NB + 4 * i + 3] = hi.w;
-                }
-                float xs = 0.0f;
-#pragma unroll
-                for (int i = 0; i < NE; ++i) xs += xv[i];
-#pragma unroll
-                for (int r = 0; r < QRW; ++r) {
-                    // low nibbles as they lie, high nibbles in place (16 n, scaled back once)
-                    float sl = 0.0f, sh = 0.0f;
-#pragma unroll
-                    for (int j = 0; j < NW; ++j) {
-                        const uint32_t lo = and_opaque(q[c][r][j], 0x0F0F0F0Fu);
-                        const uint32_t hi = and_opaque(q[c][r][j], 0xF0F0F0F0u);
-                        sl = fmaf((float)(lo & 0xFF), xv[4 * j], sl);
-                        sh = fmaf((float)(hi & 0xFF), xv[NB + 4 * j], sh);
-                        sl = fmaf((float)((lo >> 8) & 0xFF), xv[4 * j + 1], sl);
-                        sh = fmaf((float)((hi >> 8) & 0xFF), xv[NB + 4 * j + 1], sh);
-                        sl = fmaf((float)((lo >> 16) & 0xFF), xv[4 * j + 2], sl);
-                        sh = fmaf((float)((hi >> 16) & 0xFF), xv[NB + 4 * j + 2], sh);
-                        sl = fmaf((float)(lo >> 24), xv[4 * j + 3], sl);
-                        sh = fmaf((float)(hi >> 24), xv[NB + 4 * j + 3], sh);
-                    }
-                    acc[r][t] = fmaf(d[c][r], fmaf(sh, 0.0625f, sl) - 8.0f * xs, acc[r][t]);
-                }
+                for (int r = 0; r < QRW; ++r) acc[r][t] = q4_item_dot<SUB>(q[c][r], xv, d[c][r], xs, acc[r][t]);
             }
         }
     }
@@ -169,6 +237,148 @@ __device__ __forceinline__ void q4_mm_rows(const uint8_t *__restrict__ w, const 
             if (lane == 0 && r0 + r < n_out) y[(size_t)(t0 + t) * n_out + r0 + r] = v;
         }
     }
+}
+
+// Many rows (a vocabulary head): exact int8 block sums on the matrix cores. The token's activations
+// become, per block b, four int8 digits D_p (|D_p| <= 64) with
+//   x_k 2^(132 - E_b) = D_0k + D_1k 2^-7 + D_2k 2^-14 + D_3k 2^-21 (+ less than 2^-22),
+// E_b the largest biased exponent of the block's |x| (so |x_k| 2^(132 - E_b) < 64): exact for every
+// element within 2^-3 of the block's largest, and within 2^-28 of that largest for the rest. Each
+// v_mfma_i32_16x16x32_i8 then sums 16 (n - 8) D over one block's 8 elements exactly, with the
+// weights 16 (n - 8) = ((n ^ 8) << 4) as signed bytes. A step covers 16 rows x 4 blocks: K group g of
+// the instruction carries one block of each row (B, from lane (row j, group g)), and A row 4g + p
+// carries digit p of that block (zero in the other groups), so lane (j, g) receives C[4g + p][j], the
+// four digit sums of its own row and block, which it folds with its own d:
+//   acc += d * ((((C_3 2^-7 + C_2) 2^-7 + C_1) 2^-7 + C_0) * 2^(E_b - 136)),
+// the block's term d sum_k (n_k - 8) x_k up to f32 rounding. The lanes of a row add their sums in
+// a fixed order, and every token is its own pass (blockIdx.y), so a token's result does not depend
+// on the other tokens of the call. A block with a non-finite activation gives NaN rows.
+typedef int qi_v4i __attribute__((ext_vector_type(4)));
+constexpr int QI_WAVES = 4, QI_ROWS = 16, QI_CH = 2;  // waves, rows per wave, step pairs per load chunk
+constexpr int QI_MIN_ROWS = 16384, QI_MAX_NB = 256;    // rvh_q4_mm takes this kernel from 16384 rows, k <= 8192
+// dynamic LDS: digits [nb][4 digits][8 dwords], 8 zero dwords, then the block scales [nb]
+inline size_t qi_lds_bytes(int nb) { return (size_t)nb * (128 + 4) + 32; }
+
+template <bool ALN>  // rows of an even block count on a 4-byte aligned matrix (q4_rows_aligned)
+__global__ __launch_bounds__(256) void k_q4_mm_i8(const uint8_t *__restrict__ w, const float *__restrict__ x,
+                                                  float *__restrict__ y, int n_out, int k) {
+    extern __shared__ __align__(16) uint32_t qi_sh[];
+    const int nb = k / QK, tid = threadIdx.x;
+    uint32_t *dig = qi_sh, *zero = qi_sh + nb * 32;
+    float *xsc = (float *)(qi_sh + nb * 32 + 8);
+    const int lane = tid & 63, j = lane & 15, g = lane >> 4;
+    const int r0 = (blockIdx.x * QI_WAVES + (tid >> 6)) * QI_ROWS;
+    const size_t rb = (size_t)nb * Q4_BLOCK;
+    const uint8_t *wr = w + (size_t)min(r0 + j, n_out - 1) * rb;
+    // Steps go in pairs: K group g of pair p carries block 8p + 2g in the pair's first step and
+    // block 8p + 2g + 1 in its second, so each lane loads two adjacent blocks, 36 bytes of its row.
+    // This lane's A operand: digit j & 3 of its K group's block when j >> 2 == g, zeros otherwise.
+    const bool adig = (j >> 2) == g;
+    const int pairs = (nb + 7) >> 3, nch = (pairs + QI_CH - 1) / QI_CH;
+    // a pair's weights: d of both blocks and their nibble dwords, v = {d0, n0[4], d1, n1[4]}
+    auto load = [&](int c, uint32_t (&v)[QI_CH][10]) {
+#pragma unroll
+        for (int u = 0; u < QI_CH; ++u) {
+            const int b0 = (c * QI_CH + u) * 8 + 2 * g;
+            if constexpr (ALN) {
+                // blocks 2i and 2i + 1 are the 9 dwords from byte 36 i (rows of an even block count)
+                const Dwords<4> a = *(const Dwords<4> *)(wr + min(b0, nb - 2) * Q4_BLOCK);
+                const Dwords<4> e = *(const Dwords<4> *)(wr + min(b0, nb - 2) * Q4_BLOCK + 16);
+                const uint32_t f = *(const uint32_t *)(wr + min(b0, nb - 2) * Q4_BLOCK + 32);
+                const uint32_t dw[9] = {a.q[0], a.q[1], a.q[2], a.q[3], e.q[0], e.q[1], e.q[2], e.q[3], f};
+                v[u][0] = dw[0] & 0xFFFFu;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) v[u][1 + m] = __builtin_amdgcn_perm(dw[m + 1], dw[m], 0x05040302u);
+                v[u][5] = dw[4] >> 16;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) v[u][6 + m] = dw[5 + m];
+            } else {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint8_t *p = wr + min(b0 + h, nb - 1) * Q4_BLOCK;
+                    v[u][5 * h] = *(const uint16_t *)p;
+                    const Q4Nibbles<4> q = *(const Q4Nibbles<4> *)(p + 2);
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) v[u][5 * h + 1 + m] = q.q[m];
+                }
+            }
+        }
+    };
+    // the first chunk's weight loads go out before the activation digits are built
+    const bool rows_live = r0 < n_out;
+    uint32_t v0[QI_CH][10], v1[QI_CH][10];
+    if (rows_live) load(0, v0);
+    // The token's digits: a thread per 4 elements, 8 threads per block.
+    const float4 *xt = (const float4 *)(x + (size_t)blockIdx.y * k);
+    for (int f = tid; f < nb * 8; f += 256) {
+        const int blk = f >> 3, q = f & 7;
+        const float4 v = xt[f];
+        const float e4[4] = {v.x, v.y, v.z, v.w};
+        int e = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e = max(e, (int)((__float_as_uint(e4[i]) >> 23) & 0xFF));
+        e = max(e, __shfl_xor(e, 1));
+        e = max(e, __shfl_xor(e, 2));
+        e = max(e, __shfl_xor(e, 4));
+        uint32_t pk[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float u = ldexpf(e4[i], 132 - e);
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const float dp = rintf(u);
+                pk[p] |= ((uint32_t)(int)dp & 0xFFu) << (8 * i);
+                u = (u - dp) * 128.0f;
+            }
+        }
+        // elements 4q .. 4q+3 are bytes 8q .. 8q+3 of a digit's 32 (q < 4); 16 + 4m .. are 8m+4 ..
+        const int dw = q < 4 ? 2 * q : 2 * (q - 4) + 1;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) dig[(blk * 4 + p) * 8 + dw] = pk[p];
+        if (q == 0) xsc[blk] = e == 255 ? __uint_as_float(0x7FC00000u) : ldexpf(1.0f, e - 136);
+    }
+    if (tid < 8) zero[tid] = 0u;
+    __syncthreads();
+    if (!rows_live) return;
+
+    float acc = 0.0f;
+    auto compute = [&](int c, const uint32_t (&v)[QI_CH][10]) {
+#pragma unroll
+        for (int u = 0; u < QI_CH; ++u) {
+            if (c * QI_CH + u >= pairs) break;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int blk = (c * QI_CH + u) * 8 + 2 * g + h;
+                const bool live = blk < nb;
+                const uint32_t *ap = adig && live ? dig + (blk * 4 + (j & 3)) * 8 : zero;
+                const uint4 a0 = *(const uint4 *)ap, a1 = *(const uint4 *)(ap + 4);
+                const uint32_t ad[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                qi_v4i cm = {0, 0, 0, 0};
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const uint32_t t = v[u][5 * h + 1 + m] ^ 0x88888888u;
+                    const long bw = (long)(((uint64_t)(t & 0xF0F0F0F0u) << 32) | ((t << 4) & 0xF0F0F0F0u));
+                    const long aw = (long)(((uint64_t)ad[2 * m + 1] << 32) | ad[2 * m]);
+                    cm = __builtin_amdgcn_mfma_i32_16x16x32_i8(aw, bw, cm, 0, 0, 0);
+                }
+                const float t = fmaf(fmaf(fmaf((float)cm[3], 0.0078125f, (float)cm[2]), 0.0078125f, (float)cm[1]),
+                                     0.0078125f, (float)cm[0]);
+                // past the row's last block the lane adds nothing (its loaded d is another block's)
+                if (live) acc = fmaf(h2f((uint16_t)v[u][5 * h]), t * xsc[blk], acc);
+            }
+        }
+    };
+    for (int c = 0; c < nch; c += 2) {
+        if (c + 1 < nch) load(c + 1, v1);
+        compute(c, v0);
+        if (c + 1 >= nch) break;
+        if (c + 2 < nch) load(c + 2, v0);
+        compute(c + 1, v1);
+    }
+    // the four lanes of row j, groups (0 + 2) + (1 + 3)
+    float r = acc + __shfl_xor(acc, 32);
+    r = r + __shfl_xor(r, 16);
+    if (g == 0 && r0 + j < n_out) y[(size_t)blockIdx.y * n_out + r0 + j] = r;
 }
 
 template <int SUB, int NCOL, int QRW, int TT>
@@ -227,6 +437,9 @@ __global__ void k_moe_combine(const float *__restrict__ y, const int32_t *__rest
         out[(size_t)t * width + i] = acc;
     }
 }
+
+// a matrix of n_out rows of k goes through k_q4_mm_i8 (whatever the token count)
+inline bool q4_uses_i8(int n_out, int k) { return n_out >= QI_MIN_ROWS && k / QK <= QI_MAX_NB; }
 
 // rows per wave for n_out rows in all: about 2048 waves, each with as many rows' bytes in flight as
 // that allows
@@ -289,6 +502,18 @@ int rvh_f32_mm(const float *w, const float *x, float *y, int n_out, int k, int n
 int rvh_q4_mm(const void *w, const float *x, float *y, int n_out, int k, int n_in) {
     RVM_CHECK(w && x && y && n_out > 0 && n_in > 0 && k > 0 && k % QK == 0 && ((uintptr_t)w & 1) == 0);
     RVM_CHECK(grid_blocks(n_in, QTT) <= 65535);
+    if (q4_uses_i8(n_out, k)) {
+        RVM_CHECK(n_in <= 65535);
+        const int nb = k / QK;
+        const dim3 grid(grid_blocks(n_out, QI_WAVES * QI_ROWS), n_in);
+        if (q4_rows_aligned((const uint8_t *)w, nb))
+            hipLaunchKernelGGL(k_q4_mm_i8<true>, grid, dim3(256), qi_lds_bytes(nb), cur_stream(), (const uint8_t *)w,
+                               x, y, n_out, k);
+        else
+            hipLaunchKernelGGL(k_q4_mm_i8<false>, grid, dim3(256), qi_lds_bytes(nb), cur_stream(),
+                               (const uint8_t *)w, x, y, n_out, k);
+        return launched();
+    }
     const int rw = q4_rows_per_wave(n_out);
     const dim3 grid(grid_blocks(n_out, rw), grid_blocks(n_in, n_in == 1 ? 1 : QTT));
     q4_dispatch<Q4One>(k, rw, n_in, [&](auto kern) {
@@ -300,23 +525,31 @@ int rvh_q4_mm(const void *w, const float *x, float *y, int n_out, int k, int n_i
 int rvm_q4_mm_n(int n_mat, const void *const *w, const int *n_out, float *const *y, const float *x, int k, int n_in) {
     RVM_CHECK(n_mat >= 1 && n_mat <= Q4_NMAT && w && n_out && y && x && n_in > 0 && k > 0 && k % QK == 0);
     RVM_CHECK(grid_blocks(n_in, QTT) <= 65535);
+    for (int m = 0; m < n_mat; ++m) RVM_CHECK(w[m] && y[m] && n_out[m] > 0 && ((uintptr_t)w[m] & 1) == 0);
+    // matrices that rvh_q4_mm sends to k_q4_mm_i8 go there (their own launches), the rest together
+    Q4Mats mats{};
     long rows = 0;
     for (int m = 0; m < n_mat; ++m) {
-        RVM_CHECK(w[m] && y[m] && n_out[m] > 0 && ((uintptr_t)w[m] & 1) == 0);
+        if (q4_uses_i8(n_out[m], k)) continue;
+        mats.w[mats.n] = (const uint8_t *)w[m];
+        mats.y[mats.n] = y[m];
+        mats.n_out[mats.n] = n_out[m];
         rows += n_out[m];
+        ++mats.n;
     }
+    for (int m = 0; m < n_mat; ++m)
+        if (q4_uses_i8(n_out[m], k)) {
+            const int rc = rvh_q4_mm(w[m], x, y[m], n_out[m], k, n_in);
+            if (rc) return rc;
+        }
+    if (mats.n == 0) return 0;
     const int rw = q4_rows_per_wave(rows);
-    Q4Mats mats{};
     long blocks = 0;
-    for (int m = 0; m < n_mat; ++m) {
-        mats.w[m] = (const uint8_t *)w[m];
-        mats.y[m] = y[m];
-        mats.n_out[m] = n_out[m];
+    for (int m = 0; m < mats.n; ++m) {
         mats.start[m] = (int)blocks;
-        blocks += grid_blocks(n_out[m], rw);
+        blocks += grid_blocks(mats.n_out[m], rw);
     }
     RVM_CHECK(blocks <= 0x7fffffffL);
-    mats.n = n_mat;
     const dim3 grid((unsigned)blocks, grid_blocks(n_in, n_in == 1 ? 1 : QTT));
     q4_dispatch<Q4Many>(k, rw, n_in, [&](auto kern) {
         hipLaunchKernelGGL(kern, grid, dim3(64), 0, cur_stream(), mats, x, k, n_in);

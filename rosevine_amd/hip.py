@@ -402,7 +402,8 @@ def q4_mm(w: DevBuf, x: DevBuf, y: DevBuf, n_out: int, k: int, n_in: int) -> Non
 
 
 def q4_mm_n(ws: list, x: DevBuf, ys: list, n_outs: list, k: int, n_in: int) -> None:
-    """rvm_q4_mm_n: up to four rvh_q4_mm products on one input in one launch."""
+    """rvm_q4_mm_n: up to four rvh_q4_mm products on one input in one launch (a matrix of 16384
+    rows or more, k <= 8192, in a launch of its own)."""
     n = len(ws)
     if not (len(ys) == n and len(n_outs) == n):
         raise ValueError("one output and one row count per matrix")

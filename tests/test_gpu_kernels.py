@@ -251,6 +251,94 @@ def test_out_of_range_calls_are_refused(gpu):
     assert e.value.code == 1
 
 
+def dequant_q4(w, n_out, k):
+    """[n_out][k] f32 weights (n - 8) * d of Q4_0 rows (runtime/src/ops.rs:83-92; exact in f32)."""
+    blk = w.reshape(n_out, k // QK, Q4B)
+    d = blk[:, :, :2].copy().view(np.float16).astype(np.float32)  # [n_out, nb, 1]
+    q = blk[:, :, 2:]
+    n = np.concatenate([q & 0xF, q >> 4], axis=2).astype(np.float32) - 8.0  # elements j, then 16 + j
+    return (n * d).reshape(n_out, k)
+
+
+@pytest.mark.parametrize("n_out,k", [
+    (16389, 2816),   # the output head's width (contract.rs:41-62), rows past a 64-row workgroup
+    (16400, 4096),   # two steps' worth of blocks per K group more
+    (16384, 2112),   # 66 blocks: a last step with two live K groups
+    (16390, 8192),   # the largest k of this path
+    (16387, 2080),   # 65 blocks: rows not on a dword boundary (the unaligned loads)
+    (20000, 96),     # 3 blocks
+])
+def test_q4_mm_many_rows_matches_oracle(gpu, orc, n_out, k):
+    """rvh_q4_mm from 16384 rows (int8 digits of x on the matrix cores) against ops::matmul_q4_0
+    (runtime/tests/hip_ops.rs:56-81): rel L2 < 1e-5 and batch invariance; the same matrix 2 bytes
+    past a dword boundary (the unaligned loads) gives the same bits."""
+    rng = np.random.default_rng(n_out + k)
+    w = rand_q4(rng, n_out, k, 0.01, 0.03)
+    x = rng.uniform(-1, 1, (3, k)).astype(np.float32)
+    want = orc.matmul_q4_0(w, k, x, 3, n_out)
+    wd, xd, y = dev(w), dev(x), DevBuf(3 * n_out * 4)
+    hip.q4_mm(wd, xd, y, n_out, k, 3)
+    got = y.download(np.float32, 3 * n_out).reshape(3, n_out)
+    rel = np.sqrt(((got - want).astype(np.float64) ** 2).sum() / (want.astype(np.float64) ** 2).sum())
+    assert rel < 1e-5, rel
+    y1 = DevBuf(n_out * 4)
+    hip.q4_mm(wd, dev(x[2]), y1, n_out, k, 1)
+    assert np.array_equal(y1.download(np.float32, n_out), got[2])
+    off = DevBuf(w.nbytes + 2)
+    off.upload(w, 2)
+    y2 = DevBuf(n_out * 4)
+    hip.check(hip.lib().rvh_q4_mm(off.at(2, w.nbytes), xd.at(2 * k * 4, k * 4), y2.at(0, n_out * 4), n_out, k, 1))
+    assert np.array_equal(y2.download(np.float32, n_out), got[2])
+
+
+def test_q4_mm_many_rows_activation_edge_cases(gpu):
+    """The int8 digits of x across a block's range: zero and subnormal blocks, one large element
+    among tiny ones, values near 1e30, and a spread of 12 decades; each row within the reference's
+    summation bound 4e-6 sum|w x| of the exact product (expert_kernel.rs:346-348). (An element
+    below 2^-4 of its block's largest is held to 2^-28 of that largest.) A non-finite activation
+    makes every row NaN."""
+    n_out, k = 16384, 2816
+    rng = np.random.default_rng(77)
+    w = rand_q4(rng, n_out, k, 0.01, 0.03)
+    x = rng.uniform(-1, 1, (3, k)).astype(np.float32)
+    x[0, 0:32] = 0.0
+    x[0, 32:64] = rng.uniform(-1, 1, 32) * np.float32(1e-40)   # subnormal
+    x[0, 64:96] = rng.uniform(-1, 1, 32) * np.float32(1e-20)
+    x[0, 70] = 1e3                                              # one large element among tiny ones
+    x[0, 96:128] = rng.uniform(-1, 1, 32) * np.float32(1e30)
+    x[0, 128:160] = -0.0
+    x[1] = (rng.uniform(-1, 1, k) * 10.0 ** rng.uniform(-6, 6, k)).astype(np.float32)
+    x[2, 5 * 32 + 7] = np.inf
+    wf = dequant_q4(w, n_out, k).astype(np.float64)
+    y = DevBuf(3 * n_out * 4)
+    hip.q4_mm(dev(w), dev(x), y, n_out, k, 3)
+    got = y.download(np.float32, 3 * n_out).reshape(3, n_out)
+    for t in range(2):
+        xt = x[t].astype(np.float64)
+        exact = wf @ xt
+        bound = 4e-6 * (np.abs(wf) @ np.abs(xt)) + 1e-37
+        err = np.abs(got[t].astype(np.float64) - exact)
+        assert (err <= bound).all(), (t, np.argmax(err - bound), float(np.max(err / bound)))
+    assert np.isnan(got[2]).all()
+
+
+def test_q4_mm_n_with_a_many_row_matrix(gpu):
+    """rvm_q4_mm_n with a matrix of 16384+ rows among smaller ones: each output is rvh_q4_mm's."""
+    rows, k = (2048, 16400, 1000), 2816
+    rng = np.random.default_rng(5)
+    ws = [hip.DevBuf(r * (k // 32) * 18) for r in rows]
+    for i, (w, r) in enumerate(zip(ws, rows)):
+        hip.synth_q4(w, 1, r, k, 9, 70 + i)
+    for n_in in (1, 2):
+        x = dev((rng.standard_normal((n_in, k)) * 0.5).astype(np.float32))
+        ys = [hip.DevBuf(n_in * r * 4) for r in rows]
+        hip.q4_mm_n(ws, x, ys, list(rows), k, n_in)
+        for w, yb, r in zip(ws, ys, rows):
+            y1 = hip.DevBuf(n_in * r * 4)
+            hip.q4_mm(w, x, y1, r, k, n_in)
+            assert np.array_equal(yb.download(np.float32, n_in * r), y1.download(np.float32, n_in * r)), (r, n_in)
+
+
 @pytest.mark.parametrize("rows,k", [
     ((4096, 2048, 2048), 2816),   # q, k, v of a sliding-window layer (contract.rs:41-62)
     ((2112, 2112), 2816),         # gate and up
