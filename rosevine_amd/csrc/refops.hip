@@ -254,13 +254,14 @@ __device__ __forceinline__ void q4_mm_rows(const uint8_t *__restrict__ w, const 
 // a fixed order, and every token is its own pass (blockIdx.y), so a token's result does not depend
 // on the other tokens of the call. A block with a non-finite activation gives NaN rows.
 typedef int qi_v4i __attribute__((ext_vector_type(4)));
-constexpr int QI_WAVES = 4, QI_ROWS = 16, QI_CH = 2;  // waves, rows per wave, step pairs per load chunk
+constexpr int QI_WAVES = 8, QI_ROWS = 16, QI_CH = 4;  // waves, rows per wave, step pairs per load chunk
+constexpr int QI_BUF = 1;                               // chunks in registers
 constexpr int QI_MIN_ROWS = 16384, QI_MAX_NB = 256;    // rvh_q4_mm takes this kernel from 16384 rows, k <= 8192
 // dynamic LDS: digits [nb][4 digits][8 dwords], 8 zero dwords, then the block scales [nb]
 inline size_t qi_lds_bytes(int nb) { return (size_t)nb * (128 + 4) + 32; }
 
 template <bool ALN>  // rows of an even block count on a 4-byte aligned matrix (q4_rows_aligned)
-__global__ __launch_bounds__(256) void k_q4_mm_i8(const uint8_t *__restrict__ w, const float *__restrict__ x,
+__global__ __launch_bounds__(QI_WAVES * 64) void k_q4_mm_i8(const uint8_t *__restrict__ w, const float *__restrict__ x,
                                                   float *__restrict__ y, int n_out, int k) {
     extern __shared__ __align__(16) uint32_t qi_sh[];
     const int nb = k / QK, tid = threadIdx.x;
@@ -275,7 +276,9 @@ __global__ __launch_bounds__(256) void k_q4_mm_i8(const uint8_t *__restrict__ w,
     // This lane's A operand: digit j & 3 of its K group's block when j >> 2 == g, zeros otherwise.
     const bool adig = (j >> 2) == g;
     const int pairs = (nb + 7) >> 3, nch = (pairs + QI_CH - 1) / QI_CH;
-    // a pair's weights: d of both blocks and their nibble dwords, v = {d0, n0[4], d1, n1[4]}
+    // a pair's weights: aligned rows, its 9 dwords as loaded (d0 in the low half of v[0], nibbles of
+    // the first block from byte 2, d1 in the high half of v[4], nibbles of the second in v[5 .. 8]);
+    // otherwise v = {d0, n0[4], d1, n1[4]}
     auto load = [&](int c, uint32_t (&v)[QI_CH][10]) {
 #pragma unroll
         for (int u = 0; u < QI_CH; ++u) {
@@ -285,13 +288,10 @@ __global__ __launch_bounds__(256) void k_q4_mm_i8(const uint8_t *__restrict__ w,
                 const Dwords<4> a = *(const Dwords<4> *)(wr + min(b0, nb - 2) * Q4_BLOCK);
                 const Dwords<4> e = *(const Dwords<4> *)(wr + min(b0, nb - 2) * Q4_BLOCK + 16);
                 const uint32_t f = *(const uint32_t *)(wr + min(b0, nb - 2) * Q4_BLOCK + 32);
+                // the dwords as loaded: compute() picks the fields, so nothing here waits for them
                 const uint32_t dw[9] = {a.q[0], a.q[1], a.q[2], a.q[3], e.q[0], e.q[1], e.q[2], e.q[3], f};
-                v[u][0] = dw[0] & 0xFFFFu;
 #pragma unroll
-                for (int m = 0; m < 4; ++m) v[u][1 + m] = __builtin_amdgcn_perm(dw[m + 1], dw[m], 0x05040302u);
-                v[u][5] = dw[4] >> 16;
-#pragma unroll
-                for (int m = 0; m < 4; ++m) v[u][6 + m] = dw[5 + m];
+                for (int i = 0; i < 9; ++i) v[u][i] = dw[i];
             } else {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
@@ -304,30 +304,46 @@ __global__ __launch_bounds__(256) void k_q4_mm_i8(const uint8_t *__restrict__ w,
             }
         }
     };
-    // the first chunk's weight loads go out before the activation digits are built
-    const bool rows_live = r0 < n_out;
-    uint32_t v0[QI_CH][10], v1[QI_CH][10];
-    if (rows_live) load(0, v0);
-    // The token's digits: a thread per 4 elements, 8 threads per block.
+    // The token's activations first (a thread per 4 elements, 8 threads per block), then the first
+    // QI_BUF chunks of weights, in flight while the activation digits are built; chunk c + QI_BUF is
+    // loaded into chunk c's registers once chunk c is computed. (Loads past the last chunk would
+    // re-read it; with more than one chunk in registers, skipping them under a branch makes the
+    // compiler's waits on the other path wait for the newer loads too.)
+    constexpr int XPT = QI_MAX_NB * 8 / (QI_WAVES * 64);  // float4s per thread at most
     const float4 *xt = (const float4 *)(x + (size_t)blockIdx.y * k);
-    for (int f = tid; f < nb * 8; f += 256) {
+    float4 xq[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+        const int f = tid + i * QI_WAVES * 64;
+        xq[i] = f < nb * 8 ? xt[f] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const bool rows_live = r0 < n_out;
+    uint32_t vb[QI_BUF][QI_CH][10];
+#pragma unroll
+    for (int i = 0; i < QI_BUF; ++i)
+        if (i < nch) load(i, vb[i]);
+    // the digits
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+        const int f = tid + i * QI_WAVES * 64;
+        if (f >= nb * 8) break;
         const int blk = f >> 3, q = f & 7;
-        const float4 v = xt[f];
+        const float4 v = xq[i];
         const float e4[4] = {v.x, v.y, v.z, v.w};
         int e = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) e = max(e, (int)((__float_as_uint(e4[i]) >> 23) & 0xFF));
+        for (int el = 0; el < 4; ++el) e = max(e, (int)((__float_as_uint(e4[el]) >> 23) & 0xFF));
         e = max(e, __shfl_xor(e, 1));
         e = max(e, __shfl_xor(e, 2));
         e = max(e, __shfl_xor(e, 4));
         uint32_t pk[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float u = ldexpf(e4[i], 132 - e);
+        for (int el = 0; el < 4; ++el) {
+            float u = ldexpf(e4[el], 132 - e);
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 const float dp = rintf(u);
-                pk[p] |= ((uint32_t)(int)dp & 0xFFu) << (8 * i);
+                pk[p] |= ((uint32_t)(int)dp & 0xFFu) << (8 * el);
                 u = (u - dp) * 128.0f;
             }
         }
@@ -353,10 +369,21 @@ __global__ __launch_bounds__(256) void k_q4_mm_i8(const uint8_t *__restrict__ w,
                 const uint32_t *ap = adig && live ? dig + (blk * 4 + (j & 3)) * 8 : zero;
                 const uint4 a0 = *(const uint4 *)ap, a1 = *(const uint4 *)(ap + 4);
                 const uint32_t ad[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                uint32_t nib[4], dbits;
+                if constexpr (ALN) {
+#pragma unroll
+                    for (int m = 0; m < 4; ++m)
+                        nib[m] = h ? v[u][5 + m] : __builtin_amdgcn_perm(v[u][m + 1], v[u][m], 0x05040302u);
+                    dbits = h ? v[u][4] >> 16 : v[u][0] & 0xFFFFu;
+                } else {
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) nib[m] = v[u][5 * h + 1 + m];
+                    dbits = v[u][5 * h];
+                }
                 qi_v4i cm = {0, 0, 0, 0};
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
-                    const uint32_t t = v[u][5 * h + 1 + m] ^ 0x88888888u;
+                    const uint32_t t = nib[m] ^ 0x88888888u;
                     const long bw = (long)(((uint64_t)(t & 0xF0F0F0F0u) << 32) | ((t << 4) & 0xF0F0F0F0u));
                     const long aw = (long)(((uint64_t)ad[2 * m + 1] << 32) | ad[2 * m]);
                     cm = __builtin_amdgcn_mfma_i32_16x16x32_i8(aw, bw, cm, 0, 0, 0);
@@ -364,16 +391,18 @@ __global__ __launch_bounds__(256) void k_q4_mm_i8(const uint8_t *__restrict__ w,
                 const float t = fmaf(fmaf(fmaf((float)cm[3], 0.0078125f, (float)cm[2]), 0.0078125f, (float)cm[1]),
                                      0.0078125f, (float)cm[0]);
                 // past the row's last block the lane adds nothing (its loaded d is another block's)
-                if (live) acc = fmaf(h2f((uint16_t)v[u][5 * h]), t * xsc[blk], acc);
+                if (live) acc = fmaf(h2f((uint16_t)dbits), t * xsc[blk], acc);
             }
         }
     };
-    for (int c = 0; c < nch; c += 2) {
-        if (c + 1 < nch) load(c + 1, v1);
-        compute(c, v0);
-        if (c + 1 >= nch) break;
-        if (c + 2 < nch) load(c + 2, v0);
-        compute(c + 1, v1);
+    for (int c0 = 0; c0 < nch; c0 += QI_BUF) {
+#pragma unroll
+        for (int b = 0; b < QI_BUF; ++b) {
+            const int c = c0 + b;
+            if (c >= nch) break;
+            compute(c, vb[b]);
+            if (c + QI_BUF < nch) load(c + QI_BUF, vb[b]);
+        }
     }
     // the four lanes of row j, groups (0 + 2) + (1 + 3)
     float r = acc + __shfl_xor(acc, 32);
@@ -507,10 +536,10 @@ int rvh_q4_mm(const void *w, const float *x, float *y, int n_out, int k, int n_i
         const int nb = k / QK;
         const dim3 grid(grid_blocks(n_out, QI_WAVES * QI_ROWS), n_in);
         if (q4_rows_aligned((const uint8_t *)w, nb))
-            hipLaunchKernelGGL(k_q4_mm_i8<true>, grid, dim3(256), qi_lds_bytes(nb), cur_stream(), (const uint8_t *)w,
+            hipLaunchKernelGGL(k_q4_mm_i8<true>, grid, dim3(QI_WAVES * 64), qi_lds_bytes(nb), cur_stream(), (const uint8_t *)w,
                                x, y, n_out, k);
         else
-            hipLaunchKernelGGL(k_q4_mm_i8<false>, grid, dim3(256), qi_lds_bytes(nb), cur_stream(),
+            hipLaunchKernelGGL(k_q4_mm_i8<false>, grid, dim3(QI_WAVES * 64), qi_lds_bytes(nb), cur_stream(),
                                (const uint8_t *)w, x, y, n_out, k);
         return launched();
     }
