@@ -193,13 +193,17 @@ def test_split_attention_against_f64_in_the_peaked_regime(gpu, orc):
     (16, 2, 512, 0, 6000, 5000, 1),      # one chunk: no merge
     (16, 8, 256, 1024, 1028, 2000, 32),  # sliding window over a wrapped ring, 32-key chunks
     (16, 8, 256, 1024, 1028, 2000, 16),  # the new key at the end of stage 1
+    (16, 8, 256, 1024, 1028, 2000, 3),   # three chunks
+    (8, 8, 512, 0, 600, 500, 12),        # one head per kv head: 12 chunks, uneven per merging wave
+    (4, 4, 256, 0, 40, 20, 32),          # 21 keys over 32 chunks: chunks of one key, the rest empty
     (32, 2, 512, 0, 300, 250, 7),        # 16 heads of a kv head per workgroup, two head groups
     (8, 4, 128, 0, 300, 250, 5),         # another head dimension: the three operations in sequence
 ])
 def test_decode_entry_matches_store_split_and_merge(gpu, orc, nh, nkv, hd, win, cap, pos, n_chunks):
     """rvm_attn_decode: the ring bytes and the output equal rvh_kv_store + rvh_attn_split +
     rvh_attn_combine bit for bit. The token's ring slot starts as 0xff bytes (NaN scales), so a stale
-    copy of it that reached the computation would show."""
+    copy of it that reached the computation would show. A second call on the same rings (the new
+    row already in place) gives the same bits."""
     print(f"[attn decode] {nh}/{nkv}/{hd} win {win} cap {cap} pos {pos} chunks {n_chunks}", flush=True)
     rng = np.random.default_rng(pos + n_chunks + hd)
     kc, vc = q8_ring(orc, rng, cap, nkv, hd)
@@ -225,6 +229,9 @@ def test_decode_entry_matches_store_split_and_merge(gpu, orc, nh, nkv, hd, win, 
     got, want = out2.download(np.float32, nh * hd), out1.download(np.float32, nh * hd)
     assert np.all(np.isfinite(got))
     assert np.array_equal(got, want)
+    out3 = DevBuf(nh * hd * 4)
+    hip.attn_decode(dq, dk, dv, kc2, vc2, out3, part, nh, nkv, hd, pos, cap, win, n_chunks)
+    assert np.array_equal(out3.download(np.float32, nh * hd), want)
     # and the oracle's attention over the stored ring
     ref = orc.attention(q, kc1.download(np.uint8, kc.size), vc1.download(np.uint8, vc.size), nh, nkv, hd, cap, win,
                         pos, 1)
