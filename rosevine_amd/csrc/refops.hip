@@ -60,8 +60,10 @@ __global__ __launch_bounds__(256) void k_f32_mm(const float *__restrict__ w, con
 // times f32 activations, the dense GEMV/GEMM family behind rvh_q4_mm (runtime/hip/rvhip.hip; the
 // reference's k_q4_mm). Workgroup (one wave) w takes rows QRW w .. QRW w + QRW-1 (1 to 8, so that
 // there are about 2048 waves) and lane l item columns l, l + 64, ... (an item is a block or half of
-// one): each row's items are read as one contiguous run per wave (a 16- or 8-byte nibble load per
-// lane, at the block's 2-byte alignment), and a lane's activations are loaded once for the wave's rows.
+// one): each row's items are read as one contiguous run per wave, through dword-aligned loads where
+// the rows start on dwords (q4_load_items; 2-byte-aligned loads read the same bytes a third slower),
+// and a lane's activations are loaded once for the wave's rows. Matrices of 16384 rows or more take
+// k_q4_mm_i8 (int8 digits of the activations on the matrix cores) instead.
 // An item adds d * (sum_j n_j x_j - 8 sum_j x_j) with n_j its unsigned nibbles (one byte convert
 // and one fused multiply-add per element), which is sum_j ((n_j - 8) d) x_j up to rounding; the
 // reference's CPU ops are the tolerance target (runtime/tests/hip_ops.rs:56-81). Each output is
