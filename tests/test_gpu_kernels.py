@@ -291,6 +291,46 @@ def test_q4_mm_many_rows_matches_oracle(gpu, orc, n_out, k):
     assert np.array_equal(y2.download(np.float32, n_out), got[2])
 
 
+@pytest.mark.parametrize("n_out,k", [(2048, 2816), (2816, 2112), (1000, 4096), (300, 704), (4100, 256)])
+def test_q4_mm_unaligned_matrix_gives_the_same_bits(gpu, n_out, k):
+    """rvh_q4_mm under 16384 rows: the matrix 2 bytes past a dword boundary (2-byte-aligned loads)
+    gives the bits of the aligned copy (dword-aligned loads and byte permutes), 1 and 3 tokens."""
+    rng = np.random.default_rng(n_out + 7 * k)
+    w = rand_q4(rng, n_out, k, 0.01, 0.03)
+    wd = dev(w)
+    off = DevBuf(w.nbytes + 2)
+    off.upload(w, 2)
+    for n_in in (1, 3):
+        x = dev(rng.uniform(-1, 1, (n_in, k)).astype(np.float32))
+        ya, yb = DevBuf(n_in * n_out * 4), DevBuf(n_in * n_out * 4)
+        hip.q4_mm(wd, x, ya, n_out, k, n_in)
+        hip.check(hip.lib().rvh_q4_mm(off.at(2, w.nbytes), x.at(0, n_in * k * 4), yb.at(0, n_in * n_out * 4), n_out,
+                                      k, n_in))
+        assert np.array_equal(ya.download(np.float32, n_in * n_out), yb.download(np.float32, n_in * n_out))
+
+
+def test_q4_mm_many_rows_shape_sweep(gpu, orc):
+    """rvh_q4_mm from 16384 rows on seeded shapes (k of 1 to 256 blocks, odd and even block counts,
+    rows not a multiple of the 128-row workgroup, 1 to 4 tokens) against ops::matmul_q4_0 within
+    relative L2 1e-5, and each token's row against its one-token call bit for bit."""
+    rng = np.random.default_rng(2026)
+    for _ in range(6):
+        n_out = int(rng.integers(16384, 20000))
+        k = 32 * int(rng.integers(1, 257))
+        n_in = int(rng.integers(1, 5))
+        w = rand_q4(rng, n_out, k, 0.005, 0.05)
+        x = (rng.standard_normal((n_in, k)) * rng.uniform(0.1, 3.0)).astype(np.float32)
+        want = orc.matmul_q4_0(w, k, x, n_in, n_out)
+        wd, y = dev(w), DevBuf(n_in * n_out * 4)
+        hip.q4_mm(wd, dev(x), y, n_out, k, n_in)
+        got = y.download(np.float32, n_in * n_out).reshape(n_in, n_out)
+        rel = np.sqrt(((got - want).astype(np.float64) ** 2).sum() / (want.astype(np.float64) ** 2).sum())
+        assert rel < 1e-5, (n_out, k, n_in, rel)
+        y1 = DevBuf(n_out * 4)
+        hip.q4_mm(wd, dev(x[n_in - 1]), y1, n_out, k, 1)
+        assert np.array_equal(y1.download(np.float32, n_out), got[n_in - 1]), (n_out, k, n_in)
+
+
 def test_q4_mm_many_rows_activation_edge_cases(gpu):
     """The int8 digits of x across a block's range: zero and subnormal blocks, one large element
     among tiny ones, values near 1e30, and a spread of 12 decades; each row within the reference's
