@@ -329,6 +329,28 @@ def other_workload(args) -> int:
             ms1 = timed([name])
             per[name] = {"rows": n_out, "k": k, "us": round(ms1 * 1e3, 3),
                          "gb_s": round(n_out * (k // 32) * 18 / (ms1 / 1e3) / 1e9, 1)}
+        # the head for 32 sequences at once (a ragged decode step's logits): passes of 4 tokens that
+        # share the weight loads
+        hw, _, _, hrows, hk = mats["head"]
+        x32 = hip.DevBuf.from_array(rng.standard_normal((32, hk)).astype(np.float32))
+        y32 = hip.DevBuf(32 * hrows * 4)
+        hreps = 20
+        hip.Graph.begin()
+        for _ in range(hreps):
+            hip.q4_mm(hw, x32, y32, hrows, hk, 32)
+        g32 = hip.Graph.end()
+        g32.launch()
+        hip.sync()
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record()
+        g32.launch()
+        e1.record()
+        e1.synchronize()
+        g32.close()
+        ms32 = e0.elapsed_ms(e1) / hreps
+        per["head_32_tokens"] = {"rows": hrows, "k": hk, "tokens": 32, "us": round(ms32 * 1e3, 3),
+                                 "us_per_token": round(ms32 * 1e3 / 32, 3),
+                                 "weight_gb_s": round(hrows * (hk // 32) * 18 / (ms32 / 1e3) / 1e9, 1)}
         layer_names = [nm for nm, _, _ in shapes]
         ms_sep = timed(layer_names)
         ms = timed(groups, fused=True)

@@ -253,22 +253,33 @@ __device__ __forceinline__ void q4_mm_rows(const uint8_t *__restrict__ w, const 
 // four digit sums of its own row and block, which it folds with its own d:
 //   acc += d * ((((C_3 2^-7 + C_2) 2^-7 + C_1) 2^-7 + C_0) * 2^(E_b - 136)),
 // the block's term d sum_k (n_k - 8) x_k up to f32 rounding. The lanes of a row add their sums in
-// a fixed order, and every token is its own pass (blockIdx.y), so a token's result does not depend
-// on the other tokens of the call. A block with a non-finite activation gives NaN rows.
+// a fixed order, and the tokens of a pass (up to 4 per blockIdx.y) share only the weight loads, so
+// a token's result does not depend on the other tokens of the call. A block with a non-finite
+// activation gives NaN rows.
 typedef int qi_v4i __attribute__((ext_vector_type(4)));
 constexpr int QI_WAVES = 8, QI_ROWS = 16, QI_CH = 4;  // waves, rows per wave, step pairs per load chunk
 constexpr int QI_BUF = 1;                               // chunks in registers
 constexpr int QI_MIN_ROWS = 16384, QI_MAX_NB = 256;    // rvh_q4_mm takes this kernel from 16384 rows, k <= 8192
-// dynamic LDS: digits [nb][4 digits][8 dwords], 8 zero dwords, then the block scales [nb]
-inline size_t qi_lds_bytes(int nb) { return (size_t)nb * (128 + 4) + 32; }
+// dynamic LDS for tt tokens: digits [tt][nb][4 digits][8 dwords], 8 zero dwords, then the block
+// scales [tt][nb]; passes take 4, 2 or 1 tokens, as many as fit 64 KB
+inline size_t qi_lds_bytes(int nb, int tt) { return (size_t)tt * nb * (128 + 4) + 32; }
+inline int qi_tokens(int nb, int n_in) {
+    const int tt = qi_lds_bytes(nb, 4) <= 65536 ? 4 : (qi_lds_bytes(nb, 2) <= 65536 ? 2 : 1);
+    return n_in >= tt ? tt : (n_in >= 2 && tt >= 2 ? 2 : 1);
+}
 
-template <bool ALN>  // rows of an even block count on a 4-byte aligned matrix (q4_rows_aligned)
+// ALN: rows of an even block count on a 4-byte aligned matrix (q4_rows_aligned). TT: tokens per
+// pass (blockIdx.y), which share the weight loads; each has its own digits, MFMAs and folds, the
+// same operations as a pass of one token, so the same bits.
+template <bool ALN, int TT>
 __global__ __launch_bounds__(QI_WAVES * 64) void k_q4_mm_i8(const uint8_t *__restrict__ w, const float *__restrict__ x,
-                                                  float *__restrict__ y, int n_out, int k) {
+                                                  float *__restrict__ y, int n_out, int k, int n_in) {
     extern __shared__ __align__(16) uint32_t qi_sh[];
     const int nb = k / QK, tid = threadIdx.x;
-    uint32_t *dig = qi_sh, *zero = qi_sh + nb * 32;
-    float *xsc = (float *)(qi_sh + nb * 32 + 8);
+    const int t0 = blockIdx.y * TT, nt = min(TT, n_in - t0);
+    // token t's digits at dig + t nb 32, its block scales at xsc + t nb, one zero area after them
+    uint32_t *dig = qi_sh, *zero = qi_sh + TT * nb * 32;
+    float *xsc = (float *)(qi_sh + TT * nb * 32 + 8);
     const int lane = tid & 63, j = lane & 15, g = lane >> 4;
     const int r0 = (blockIdx.x * QI_WAVES + (tid >> 6)) * QI_ROWS;
     const size_t rb = (size_t)nb * Q4_BLOCK;
@@ -311,13 +322,16 @@ __global__ __launch_bounds__(QI_WAVES * 64) void k_q4_mm_i8(const uint8_t *__res
     // loaded into chunk c's registers once chunk c is computed. (Loads past the last chunk would
     // re-read it; with more than one chunk in registers, skipping them under a branch makes the
     // compiler's waits on the other path wait for the newer loads too.)
-    constexpr int XPT = QI_MAX_NB * 8 / (QI_WAVES * 64);  // float4s per thread at most
-    const float4 *xt = (const float4 *)(x + (size_t)blockIdx.y * k);
-    float4 xq[XPT];
+    constexpr int XPT = QI_MAX_NB * 8 / (QI_WAVES * 64);  // float4s per thread and token at most
+    float4 xq[TT][XPT];
 #pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-        const int f = tid + i * QI_WAVES * 64;
-        xq[i] = f < nb * 8 ? xt[f] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int t = 0; t < TT; ++t) {
+        const float4 *xt = (const float4 *)(x + (size_t)(t0 + min(t, nt - 1)) * k);
+#pragma unroll
+        for (int i = 0; i < XPT; ++i) {
+            const int f = tid + i * QI_WAVES * 64;
+            xq[t][i] = f < nb * 8 ? xt[f] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
     }
     const bool rows_live = r0 < n_out;
     uint32_t vb[QI_BUF][QI_CH][10];
@@ -326,11 +340,13 @@ __global__ __launch_bounds__(QI_WAVES * 64) void k_q4_mm_i8(const uint8_t *__res
         if (i < nch) load(i, vb[i]);
     // the digits
 #pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
     for (int i = 0; i < XPT; ++i) {
         const int f = tid + i * QI_WAVES * 64;
-        if (f >= nb * 8) break;
-        const int blk = f >> 3, q = f & 7;
-        const float4 v = xq[i];
+        if (t >= nt || f >= nb * 8) break;
+        const int blk = t * nb + (f >> 3), q = f & 7;
+        const float4 v = xq[t][i];
         const float e4[4] = {v.x, v.y, v.z, v.w};
         int e = 0;
 #pragma unroll
@@ -359,7 +375,9 @@ __global__ __launch_bounds__(QI_WAVES * 64) void k_q4_mm_i8(const uint8_t *__res
     __syncthreads();
     if (!rows_live) return;
 
-    float acc = 0.0f;
+    float acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = 0.0f;
     auto compute = [&](int c, const uint32_t (&v)[QI_CH][10]) {
 #pragma unroll
         for (int u = 0; u < QI_CH; ++u) {
@@ -368,9 +386,6 @@ __global__ __launch_bounds__(QI_WAVES * 64) void k_q4_mm_i8(const uint8_t *__res
             for (int h = 0; h < 2; ++h) {
                 const int blk = (c * QI_CH + u) * 8 + 2 * g + h;
                 const bool live = blk < nb;
-                const uint32_t *ap = adig && live ? dig + (blk * 4 + (j & 3)) * 8 : zero;
-                const uint4 a0 = *(const uint4 *)ap, a1 = *(const uint4 *)(ap + 4);
-                const uint32_t ad[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
                 uint32_t nib[4], dbits;
                 if constexpr (ALN) {
 #pragma unroll
@@ -382,18 +397,31 @@ __global__ __launch_bounds__(QI_WAVES * 64) void k_q4_mm_i8(const uint8_t *__res
                     for (int m = 0; m < 4; ++m) nib[m] = v[u][5 * h + 1 + m];
                     dbits = v[u][5 * h];
                 }
-                qi_v4i cm = {0, 0, 0, 0};
+                long bw[4];
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
-                    const uint32_t t = nib[m] ^ 0x88888888u;
-                    const long bw = (long)(((uint64_t)(t & 0xF0F0F0F0u) << 32) | ((t << 4) & 0xF0F0F0F0u));
-                    const long aw = (long)(((uint64_t)ad[2 * m + 1] << 32) | ad[2 * m]);
-                    cm = __builtin_amdgcn_mfma_i32_16x16x32_i8(aw, bw, cm, 0, 0, 0);
+                    const uint32_t n8 = nib[m] ^ 0x88888888u;
+                    bw[m] = (long)(((uint64_t)(n8 & 0xF0F0F0F0u) << 32) | ((n8 << 4) & 0xF0F0F0F0u));
                 }
-                const float t = fmaf(fmaf(fmaf((float)cm[3], 0.0078125f, (float)cm[2]), 0.0078125f, (float)cm[1]),
-                                     0.0078125f, (float)cm[0]);
-                // past the row's last block the lane adds nothing (its loaded d is another block's)
-                if (live) acc = fmaf(h2f((uint16_t)dbits), t * xsc[blk], acc);
+                const float dv = h2f((uint16_t)dbits);
+#pragma unroll
+                for (int tk = 0; tk < TT; ++tk) {
+                    if (tk >= nt) break;
+                    const uint32_t *ap = adig && live ? dig + ((tk * nb + blk) * 4 + (j & 3)) * 8 : zero;
+                    const uint4 a0 = *(const uint4 *)ap, a1 = *(const uint4 *)(ap + 4);
+                    const uint32_t ad[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                    qi_v4i cm = {0, 0, 0, 0};
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        const long aw = (long)(((uint64_t)ad[2 * m + 1] << 32) | ad[2 * m]);
+                        cm = __builtin_amdgcn_mfma_i32_16x16x32_i8(aw, bw[m], cm, 0, 0, 0);
+                    }
+                    const float t = fmaf(fmaf(fmaf((float)cm[3], 0.0078125f, (float)cm[2]), 0.0078125f,
+                                              (float)cm[1]),
+                                         0.0078125f, (float)cm[0]);
+                    // past the row's last block the lane adds nothing (its loaded d is another block's)
+                    if (live) acc[tk] = fmaf(dv, t * xsc[tk * nb + blk], acc[tk]);
+                }
             }
         }
     };
@@ -407,9 +435,13 @@ __global__ __launch_bounds__(QI_WAVES * 64) void k_q4_mm_i8(const uint8_t *__res
         }
     }
     // the four lanes of row j, groups (0 + 2) + (1 + 3)
-    float r = acc + __shfl_xor(acc, 32);
-    r = r + __shfl_xor(r, 16);
-    if (g == 0 && r0 + j < n_out) y[(size_t)blockIdx.y * n_out + r0 + j] = r;
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        if (t >= nt) break;
+        float r = acc[t] + __shfl_xor(acc[t], 32);
+        r = r + __shfl_xor(r, 16);
+        if (g == 0 && r0 + j < n_out) y[(size_t)(t0 + t) * n_out + r0 + j] = r;
+    }
 }
 
 template <int SUB, int NCOL, int QRW, int TT>
@@ -535,14 +567,16 @@ int rvh_q4_mm(const void *w, const float *x, float *y, int n_out, int k, int n_i
     RVM_CHECK(grid_blocks(n_in, QTT) <= 65535);
     if (q4_uses_i8(n_out, k)) {
         RVM_CHECK(n_in <= 65535);
-        const int nb = k / QK;
-        const dim3 grid(grid_blocks(n_out, QI_WAVES * QI_ROWS), n_in);
-        if (q4_rows_aligned((const uint8_t *)w, nb))
-            hipLaunchKernelGGL(k_q4_mm_i8<true>, grid, dim3(QI_WAVES * 64), qi_lds_bytes(nb), cur_stream(), (const uint8_t *)w,
-                               x, y, n_out, k);
-        else
-            hipLaunchKernelGGL(k_q4_mm_i8<false>, grid, dim3(QI_WAVES * 64), qi_lds_bytes(nb), cur_stream(),
-                               (const uint8_t *)w, x, y, n_out, k);
+        const int nb = k / QK, tt = qi_tokens(nb, n_in);
+        const dim3 grid(grid_blocks(n_out, QI_WAVES * QI_ROWS), grid_blocks(n_in, tt));
+        const bool aln = q4_rows_aligned((const uint8_t *)w, nb);
+        auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, dim3(QI_WAVES * 64), qi_lds_bytes(nb, tt), cur_stream(), (const uint8_t *)w,
+                               x, y, n_out, k, n_in);
+        };
+        if (tt == 4) aln ? go(k_q4_mm_i8<true, 4>) : go(k_q4_mm_i8<false, 4>);
+        else if (tt == 2) aln ? go(k_q4_mm_i8<true, 2>) : go(k_q4_mm_i8<false, 2>);
+        else aln ? go(k_q4_mm_i8<true, 1>) : go(k_q4_mm_i8<false, 1>);
         return launched();
     }
     const int rw = q4_rows_per_wave(n_out);
