@@ -566,8 +566,8 @@ int rvh_q4_mm(const void *w, const float *x, float *y, int n_out, int k, int n_i
     RVM_CHECK(w && x && y && n_out > 0 && n_in > 0 && k > 0 && k % QK == 0 && ((uintptr_t)w & 1) == 0);
     RVM_CHECK(grid_blocks(n_in, QTT) <= 65535);
     if (q4_uses_i8(n_out, k)) {
-        RVM_CHECK(n_in <= 65535);
         const int nb = k / QK, tt = qi_tokens(nb, n_in);
+        RVM_CHECK(grid_blocks(n_in, tt) <= 65535);
         const dim3 grid(grid_blocks(n_out, QI_WAVES * QI_ROWS), grid_blocks(n_in, tt));
         const bool aln = q4_rows_aligned((const uint8_t *)w, nb);
         auto go = [&](auto kern) {
