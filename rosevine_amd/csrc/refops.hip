@@ -504,23 +504,27 @@ __global__ void k_moe_combine(const float *__restrict__ y, const int32_t *__rest
 // a matrix of n_out rows of k goes through k_q4_mm_i8 (whatever the token count)
 inline bool q4_uses_i8(int n_out, int k) { return n_out >= QI_MIN_ROWS && k / QK <= QI_MAX_NB; }
 
-// rows per wave for n_out rows in all: about 2048 waves, each with as many rows' bytes in flight as
-// that allows
-inline int q4_rows_per_wave(long n_out) { return n_out >= 16384 ? 8 : (n_out >= 8192 ? 4 : (n_out >= 4096 ? 2 : 1)); }
+// rows per wave for n_out rows in all: 1024 to 2048 waves, each with as many rows' bytes in flight
+// as that allows (two rows from 2048: one activation read serves both, 2816 x 4096 took 4.2 against
+// 5.2 us with one)
+inline int q4_rows_per_wave(long n_out) { return n_out >= 16384 ? 8 : (n_out >= 8192 ? 4 : (n_out >= 2048 ? 2 : 1)); }
 
 // Calls go(kernel template instance) with the instance for (k, rows per wave rw, n_in). Half-block
-// items where they take fewer lane passes than whole blocks: 1 .. 32 blocks (one column of halves
-// against one of blocks at twice the work) and 65 .. 96 (three columns of halves against two of
-// blocks). The choice depends on k alone, so every token of a batch sums in the same order.
+// items up to 128 blocks: 1 .. 32 blocks (one column of halves against one of blocks at twice the
+// work), 65 .. 96 (three columns of halves against two of blocks) and 97 .. 128 (four columns of
+// halves, the same lane passes as two of blocks, at half each lane's dependent chain: 2816 x 4096
+// took 5.2 against 7.0 us). The choice depends on k alone, so every token of a batch sums in the
+// same order.
 template <template <int, int, int, int> class K, typename Go>
 void q4_dispatch(int k, int rw, int n_in, Go &&go) {
     const int nb = k / QK, ncol = min(grid_blocks(nb, 64), 4);
-    const bool halves = nb <= 32 || (nb > 64 && nb <= 96);
+    const bool halves = nb <= 32 || (nb > 64 && nb <= 128);
     auto by_cols = [&](auto rwc, auto ttc) {
         constexpr int RW = decltype(rwc)::value, T = decltype(ttc)::value;
         if (halves) {
             if (nb <= 32) go(K<2, 1, RW, T>::fn);
-            else go(K<2, 3, RW, T>::fn);
+            else if (nb <= 96) go(K<2, 3, RW, T>::fn);
+            else go(K<2, 4, RW, T>::fn);
         } else if (ncol == 1) go(K<1, 1, RW, T>::fn);
         else if (ncol == 2) go(K<1, 2, RW, T>::fn);
         else if (ncol == 3) go(K<1, 3, RW, T>::fn);
