@@ -105,7 +105,7 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
     constexpr int XI = (R * XU + NT - 1) / NT, SI = (R * KC + NT - 1) / NT;
     constexpr int SPL = KC * 16 * NR / 64;  // weight scales per lane per chunk (2, 4 or 8)
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
-    const int w = threadIdx.x >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nb = width / QK, nch = (nb + KC - 1) / KC;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -125,7 +125,9 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
     const int skb = lane / LPB, sj = (lane % LPB) * SPL;
     // this thread's staging items, fixed over the chunks: activation piece q of tile place xrow[k],
     // and the scale of place srow[k] at chunk block skbx[k]
-    const int8_t *xsrc[XI];
+    // (32-bit offsets from the scalar bases src and ssrc: the rows are at most 65535 x 8 pairs of
+    // 1024 bytes, or tokens of 4096)
+    uint32_t xsrc[XI];
     int xq[XI], xdst[XI];
     bool xok[XI];
 #pragma unroll
@@ -133,11 +135,11 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
         const int i = threadIdx.x + k * NT, ii = min(i, R * XU - 1);
         const int row = ii / XU, q = ii - row * XU, from = sh.row_of[row];
         xok[k] = i < R * XU && from >= 0;
-        xsrc[k] = src + (size_t)(from >= 0 ? from : 0) * width;
+        xsrc[k] = (uint32_t)(from >= 0 ? from : 0) * (uint32_t)width;
         xq[k] = q * 16;
         xdst[k] = i < R * XU ? row * XP + q * 16 : -1;
     }
-    const float *ssp[SI];
+    uint32_t ssp[SI];
     int skbx[SI];
     bool sok[SI];
 #pragma unroll
@@ -145,16 +147,17 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
         const int i = threadIdx.x + k * NT, ii = min(i, R * KC - 1);
         const int kb = ii / R, row = ii - kb * R, from = sh.row_of[row];
         sok[k] = i < R * KC && from >= 0;
-        ssp[k] = ssrc + (size_t)(from >= 0 ? from : 0) * nb;
+        ssp[k] = (uint32_t)(from >= 0 ? from : 0) * (uint32_t)nb;
         skbx[k] = i < R * KC ? kb : -1;
     }
 
+    const int loff = m * 16 + 4 * g;  // this lane's byte in a piece of 16 plane entries
     auto load_w = [&](int c, uint32_t (&wn)[KC][NR], uint32_t (&wsc)[SPL / 2]) {
 #pragma unroll
         for (int kb = 0; kb < KC; ++kb) {
-            const size_t e0 = entry(c * KC + kb);
+            const uint8_t *pb = nib + entry(c * KC + kb) * 16;  // wave-uniform: a scalar base
 #pragma unroll
-            for (int r = 0; r < NR; ++r) wn[kb][r] = *(const uint32_t *)(nib + (e0 + 16 * r + m) * 16 + 4 * g);
+            for (int r = 0; r < NR; ++r) wn[kb][r] = *(const uint32_t *)(pb + (256 * r + loff));
         }
         const uint16_t *sp = scl + entry(c * KC + skb) + sj;
         if constexpr (SPL == 8) {
@@ -173,9 +176,10 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
     };
     auto load_x = [&](int c, uint4 (&xr)[XI], float (&sr)[SI]) {
 #pragma unroll
-        for (int k = 0; k < XI; ++k) xr[k] = *(const uint4 *)(xsrc[k] + min(c * KC * QK + xq[k], width - 16));
+        for (int k = 0; k < XI; ++k)
+            xr[k] = *(const uint4 *)(src + (xsrc[k] + (uint32_t)min(c * KC * QK + xq[k], width - 16)));
 #pragma unroll
-        for (int k = 0; k < SI; ++k) sr[k] = ssp[k][min(c * KC + max(skbx[k], 0), nb - 1)];
+        for (int k = 0; k < SI; ++k) sr[k] = ssrc[ssp[k] + (uint32_t)min(c * KC + max(skbx[k], 0), nb - 1)];
     };
     auto store_x = [&](int c, int buf, const uint4 (&xr)[XI], const float (&sr)[SI]) {
 #pragma unroll
@@ -294,7 +298,8 @@ __global__ __launch_bounds__(MW * 64) void k_gateup_mfma(const uint8_t *__restri
     const int nb = d / QK, Tg = ff / 32;
     if (threadIdx.x < R) sh.row_of[threadIdx.x] = (int)threadIdx.x < cnt ? order[k0 + threadIdx.x] / top_k : -1;
     __syncthreads();
-    const int rt = blockIdx.x * MW + (threadIdx.x >> 6);
+    // wave-uniform, so that the weight addresses are a scalar base and a lane offset
+    const int rt = blockIdx.x * MW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool active = rt < Tg;
     float acc[MT][4][4];
     // every m-tile, also an empty one: a second instance of the loop for tiles of at most 16 pairs
@@ -344,7 +349,7 @@ __global__ __launch_bounds__(MW * 64) void k_down_mfma(const uint8_t *__restrict
     const int Sd = ff / 64, Td = d / 32;
     if (threadIdx.x < R) sh.row_of[threadIdx.x] = (int)threadIdx.x < cnt ? k0 + (int)threadIdx.x : -1;
     __syncthreads();
-    const int rt = blockIdx.x * MW + (threadIdx.x >> 6);
+    const int rt = blockIdx.x * MW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const bool active = rt < Td;
     float acc[MT][2][4];
     // a tile runs the loop of its occupied m-tiles only
