@@ -892,36 +892,38 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
     out[(size_t)i * hd + d] = num * (1.0f / dsum);
 }
 
-// The same merge for up to 4 * CM_W chunks in one round of loads: wave w takes chunks w, w + 4, ..
-// (at most CM_W), every value and lane k's (max, sum) of its k-th chunk loaded at once; the wave's
-// maximum M_w, then o_w = sum_k e^(m_k - M_w) acc_k and l_w likewise in chunk order, and the four
-// waves' (M, l, o) merge as in k_attn_combine.
-constexpr int CM_W = 32;
-__global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ part, float *__restrict__ out, int hd,
-                                                    int n_chunks) {
-    __shared__ float wm[AT_WAVES], wl[AT_WAVES], wo[AT_WAVES][64];
+// The same merge for up to NW * CW chunks in one round of loads: wave w takes chunks w, w + NW, ..
+// (at most CW), every value and lane k's (max, sum) of its k-th chunk loaded at once; the wave's
+// maximum M_w, then o_w = sum_k e^(m_k - M_w) acc_k and l_w likewise in chunk order, and the NW
+// waves' (M, l, o) merge in wave order as in k_attn_combine. Four waves of 32 chunks take up to
+// 128 chunks, eight of 40 up to 320 (a global layer split into chunks of 64 keys at depth 16384).
+template <int NW, int CW>
+__global__ __launch_bounds__(NW * 64) void k_attn_merge(const float *__restrict__ part, float *__restrict__ out, int hd,
+                                                        int n_chunks) {
+    static_assert(CW <= 64, "one chunk's (max, sum) per lane");
+    __shared__ float wm[NW], wl[NW], wo[NW][64];
     const int i = blockIdx.x, lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int d = blockIdx.y * 64 + lane;
     const int dd = d < hd ? d : 0;
     const size_t stride = (size_t)hd + 2;
     const float *pp = part + (size_t)i * n_chunks * stride;
-    const int nw = n_chunks > w ? (n_chunks - w + AT_WAVES - 1) / AT_WAVES : 0;  // this wave's chunks
+    const int nw = n_chunks > w ? (n_chunks - w + NW - 1) / NW : 0;  // this wave's chunks
     // clamped, always valid: past the wave's chunks its first one, or the row's last one if it has none
-    auto chunk = [&](int k) { return k < nw ? w + AT_WAVES * k : min(w, n_chunks - 1); };
-    float a[CM_W];
+    auto chunk = [&](int k) { return k < nw ? w + NW * k : min(w, n_chunks - 1); };
+    float a[CW];
 #pragma unroll
-    for (int k = 0; k < CM_W; ++k) a[k] = pp[(size_t)chunk(k) * stride + 2 + dd];
-    const int kl = lane < CM_W ? lane : 0;
+    for (int k = 0; k < CW; ++k) a[k] = pp[(size_t)chunk(k) * stride + 2 + dd];
+    const int kl = lane < CW ? lane : 0;
     const float ml = pp[(size_t)chunk(kl) * stride], ll = pp[(size_t)chunk(kl) * stride + 1];
     const float mk = lane < nw ? ml : -INFINITY;
     float M = mk;
 #pragma unroll
-    for (int k = 0; k < CM_W; ++k) M = fmaxf(M, readlane_f(mk, k));
+    for (int k = 0; k < CW; ++k) M = fmaxf(M, readlane_f(mk, k));
     const float e = mk == -INFINITY ? 0.0f : expf(mk - M);  // 0 past the wave's chunks and for empty ones
     float o = 0.0f, den = 0.0f;
 #pragma unroll
-    for (int k = 0; k < CM_W; ++k) {
+    for (int k = 0; k < CW; ++k) {
         const float ek = readlane_f(e, k);
         o = fmaf(ek, a[k], o);
         den = fmaf(ek, readlane_f(ll, k), den);
@@ -933,10 +935,12 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ pa
     wo[w][lane] = o;
     __syncthreads();
     if (w != 0 || d >= hd) return;
-    const float Mx = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    float Mx = wm[0];
+#pragma unroll
+    for (int u = 1; u < NW; ++u) Mx = fmaxf(Mx, wm[u]);
     float num = 0.0f, dsum = 0.0f;
 #pragma unroll
-    for (int u = 0; u < AT_WAVES; ++u) {
+    for (int u = 0; u < NW; ++u) {
         const float eu = wm[u] == -INFINITY ? 0.0f : expf(wm[u] - Mx);
         num = fmaf(eu, wo[u][lane], num);
         dsum = fmaf(eu, wl[u], dsum);
@@ -1118,9 +1122,12 @@ int rvh_attn_split(const float *q, const void *kc, const void *vc, float *out, f
 
 int rvh_attn_combine(const float *part, float *out, int rows, int hd, int n_chunks) {
     RVM_CHECK(part && out && rows > 0 && hd > 0 && n_chunks > 1);
-    if (n_chunks > AT_WAVES * CB_B && n_chunks <= AT_WAVES * CM_W)  // more than one batch of k_attn_combine
-        hipLaunchKernelGGL(k_attn_merge, dim3(rows, (hd + 63) / 64), dim3(AT_WAVES * 64), 0, cur_stream(), part, out,
-                           hd, n_chunks);
+    if (n_chunks > AT_WAVES * CB_B && n_chunks <= 4 * 32)  // more than one batch of k_attn_combine
+        hipLaunchKernelGGL((k_attn_merge<4, 32>), dim3(rows, (hd + 63) / 64), dim3(4 * 64), 0, cur_stream(), part,
+                           out, hd, n_chunks);
+    else if (n_chunks > 4 * 32 && n_chunks <= 8 * 40)
+        hipLaunchKernelGGL((k_attn_merge<8, 40>), dim3(rows, (hd + 63) / 64), dim3(8 * 64), 0, cur_stream(), part,
+                           out, hd, n_chunks);
     else
         hipLaunchKernelGGL(k_attn_combine, dim3(rows, (hd + 63) / 64), dim3(AT_WAVES * 64), 0, cur_stream(), part,
                            out, hd, n_chunks);

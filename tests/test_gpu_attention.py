@@ -133,6 +133,10 @@ def test_split_attention_rejects_ranges_beyond_the_ring(gpu):
     (16, 4, 384, 33, 40, 1000, 3, 3),    # window, wrapped ring
     (4, 2, 160, 0, 20, 20, 1, 50),       # more chunks than keys: empty chunks merge to nothing
     (8, 2, 512, 0, 1, 1, 1, 1),          # one key: the value row itself
+    (16, 2, 512, 0, 5000, 5000, 1, 200),  # 129 .. 320 chunks: the eight-wave merge
+    (8, 2, 256, 0, 2600, 2600, 1, 320),  # its largest count
+    (4, 2, 64, 0, 150, 150, 1, 250),     # there, with 100 empty chunks
+    (4, 2, 64, 0, 400, 400, 1, 321),     # past it: the batched merge
 ])
 def test_split_attention_shapes_and_chunkings(gpu, orc, nh, nkv, hd, win, cap, total, n, n_chunks):
     print(f"[attn] shape {nh}/{nkv}/{hd} win {win} cap {cap} total {total} n {n} chunks {n_chunks}", flush=True)
