@@ -202,6 +202,8 @@ def test_split_attention_against_f64_in_the_peaked_regime(gpu, orc):
     (4, 4, 256, 0, 40, 20, 32),          # 21 keys over 32 chunks: chunks of one key, the rest empty
     (32, 2, 512, 0, 300, 250, 7),        # 16 heads of a kv head per workgroup, two head groups
     (8, 4, 128, 0, 300, 250, 5),         # another head dimension: the three operations in sequence
+    (16, 2, 512, 0, 6000, 5000, 200),    # 200 chunks of 26 keys: the eight-wave merge
+    (16, 8, 256, 1024, 1028, 2000, 256),  # the sliding window in 256 chunks of 4 keys
 ])
 def test_decode_entry_matches_store_split_and_merge(gpu, orc, nh, nkv, hd, win, cap, pos, n_chunks):
     """rvm_attn_decode: the ring bytes and the output equal rvh_kv_store + rvh_attn_split +
