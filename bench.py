@@ -82,16 +82,23 @@ def cpu_baseline(seed: int, n_tokens: int, seconds: float, threads: int):
     w = np.empty((1, synth.TOP_K), np.float32)
     for t in range(2):  # warmup
         pool.layer(router, None, None, x[t], synth.D, synth.FF, synth.TOP_K, out, ids, w)
-    done, t0 = 0, time.perf_counter()
+    done, t0, ex0 = 0, time.perf_counter(), pool.expert_seconds()
     while done < n_tokens and time.perf_counter() - t0 < seconds:
         pool.layer(router, None, None, x[done], synth.D, synth.FF, synth.TOP_K, out, ids, w)
         done += 1
     dt = time.perf_counter() - t0
+    experts_s = pool.expert_seconds() - ex0
     pool.close()
     host = host_cpu()
     return {"value": round(done / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{done} decode tokens of the same workload in {dt:.1f} s "
                       f"({'avx2_q8' if orc.CpuBaseline.uses_avx2() else 'scalar'} kernel, {threads} threads)",
+            "ms_per_token": round(dt * 1e3 / done, 4),
+            "experts_only_ms_per_token": round(experts_s * 1e3 / done, 4),
+            "experts_only_note": "the expert part alone (plan, quantisation, the pooled gate/up and down GEMVs, "
+                                 "GeGLU, combine), without the router and selection on the caller thread: the "
+                                 "span the reference's CPU expert figure covers (docs/cpu-experts-q8.md:115-123, "
+                                 "0.84 ms per layer on a 6-core 7600X)",
             "cpu_model": host["model"], "host_cpus": host["cpus"], "usable_cpus": host["usable"],
             "cores_note": f"{threads} worker threads: the GPU host's CPU share for one GPU is 16 threads, "
                           f"whatever nproc reports ({host['usable']} here)" if threads < host["usable"] else
@@ -160,6 +167,7 @@ def measure_stack30(seed: int, n_layers: int = 30, n_tok: int = 40):
     ms = e0.elapsed_ms(e1) / (n_tok - 4)
     for g in [warm] + timed:
         g.close()
+    spans = stack_spans(s, x, out, n_layers, n_tok)
     s.close()
     hip.Stream.use_default()
     stream.close()
@@ -168,7 +176,48 @@ def measure_stack30(seed: int, n_layers: int = 30, n_tok: int = 40):
         for b in (ly.gate_up, ly.down, ly.router, ly.bias):
             if b is not None:
                 b.close()
-    return ms, resident, calls
+    return ms, resident, calls, spans
+
+
+def stack_spans(s, x, out, n_layers: int, n_tok: int) -> dict:
+    """Per-layer device time of the reference's decode spans (runtime/src/instr.rs:98-132) through the
+    session's probe events: "router" from a layer's start to its router work issued, "gpu_experts" from
+    there to the layer's end, "exp_meta" 0 (no dispatch metadata is uploaded). One token per graph,
+    captured with the probe's events as event nodes, replayed once to warm and once measured, for 8
+    tokens; the mean over tokens and layers."""
+    from rosevine_amd import hip
+
+    ev = [hip.Event() for _ in range(2 * n_layers + 1)]
+    nb = s.d * 4
+    router, experts, total = [], [], []
+    s.probe(ev)
+    try:
+        for t in range(8):
+            hip.Graph.begin()
+            try:
+                s.eval(x, out, 1, x_off=(t % n_tok) * nb)
+            finally:
+                g = hip.Graph.end()
+            g.launch()
+            hip.sync()
+            g.launch()
+            ev[-1].synchronize()
+            g.close()
+            r = [ev[2 * l].elapsed_ms(ev[2 * l + 1]) * 1e3 for l in range(n_layers)]
+            e = [ev[2 * l + 1].elapsed_ms(ev[2 * l + 2]) * 1e3 for l in range(n_layers)]
+            router.append(sum(r) / n_layers)
+            experts.append(sum(e) / n_layers)
+            total.append(ev[0].elapsed_ms(ev[-1]) * 1e3 / n_layers)
+    except hip.DeviceError as err:
+        return {"error": f"probe events in a captured graph: {err}"}
+    finally:
+        s.probe(None)
+    return {"router_us_per_layer": round(sum(router) / len(router), 3),
+            "gpu_experts_us_per_layer": round(sum(experts) / len(experts), 3), "exp_meta_us_per_layer": 0.0,
+            "probed_us_per_layer": round(sum(total) / len(total), 3),
+            "note": "each event node adds about 3 us to the span it closes, so the probed layer is longer than the "
+                    "unprobed one (us_per_layer); the spans show the split, not the unprobed times",
+            "method": "rvm_session_probe events as graph nodes, one token per graph, mean of 8 tokens"}
 
 
 def measure_ragged_stack30(seed: int, n_layers: int = 30, n_tok: int = 32, steps: int = 20):
@@ -219,6 +268,121 @@ def measure_ragged_stack30(seed: int, n_layers: int = 30, n_tok: int = 32, steps
     return ms, distinct
 
 
+def measure_batch(seed: int, n: int, routing: str, steps: int, stack: bool = False) -> dict:
+    """One layer's forward over n tokens (rvm_moe_forward) on the current (non-default) stream: a graph
+    of 4 calls on 4 resident batches, replayed steps / 4 times after one warm-up replay and timed with
+    HIP events on that stream. routing:
+    "iid" (no bias), "skewed" (the 30-layer configuration's per-expert bias N(0,1): groups of 0 to a few
+    hundred pairs, some experts empty) or "zipf" (Zipf(1.1) popularity). Reports the time, the HBM and
+    int8 fractions, and the group sizes of the first batch; with stack, also the same step through 30
+    layers (cache-cold)."""
+    from rosevine_amd import hip, moe, synth
+
+    E, K8, D, FF = synth.N_EXP, synth.TOP_K, synth.D, synth.FF
+    bias = {"iid": None, "skewed": synth.router_bias(seed, 0), "zipf": synth.zipf_bias(seed)}[routing]
+    layer = moe.MoeLayer(E, K8, D, FF, synth.router_weights(seed, 0), bias)
+    layer.synth_weights(seed, synth.gate_up_stream(0), synth.down_stream(0))
+    xs = [hip.DevBuf.from_array(synth.tokens(seed + 200 + i, n)) for i in range(4)]
+    out = hip.DevBuf(n * D * 4)
+    ws = moe.Workspace(layer, n)
+    it = [0]
+
+    def run():
+        moe.forward(layer, xs[it[0] % 4], out, n, ws)
+        it[0] += 1
+
+    # graph-launched like the decode line: one graph of the 4 batches, replayed
+    hip.Graph.begin()
+    for _ in range(4):
+        run()
+    g = hip.Graph.end()
+    reps = max(1, steps // 4)
+    ms = _timed(g.launch, reps, 1) / 4
+    g.close()
+    moe.forward(layer, xs[0], out, n, ws)
+    ids, _ = ws.selection(layer, n)
+    import numpy as np
+    groups = np.bincount(ids.reshape(-1), minlength=E)
+    distinct = int((groups > 0).sum())
+    nbytes = distinct * EXPERT_BYTES + ROUTER_BYTES
+    ops = n * K8 * 2 * (2 * FF * D + D * FF)  # int8 multiply-adds x 2 per token-expert pair
+    res = {"tokens": n, "routing": {"iid": "iid router logits", "skewed": "per-expert router bias N(0,1)",
+                                    "zipf": "Zipf(1.1) router bias"}[routing],
+           "steps": 4 * max(1, steps // 4), "us": round(ms * 1e3, 2), "tokens_per_s": round(n / (ms / 1e3), 1),
+           "distinct_experts": distinct, "empty_experts": int(E - distinct),
+           "group_pairs_min_max": [int(groups.min()), int(groups.max())],
+           "hbm_gb_s": round(nbytes / (ms / 1e3) / 1e9, 1),
+           "frac_of_hbm_peak": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_step": nbytes,
+           "int8_tops": round(ops / (ms / 1e3) / 1e12, 2),
+           "int8_frac_of_5000_tops": round(ops / (ms / 1e3) / 5.0e15, 5)}
+    for b in [out, ws.buf] + xs:
+        b.close()
+    for b in (layer.gate_up, layer.down, layer.router, layer.bias):
+        if b is not None:
+            b.close()
+    if stack:
+        log(f"[bench] ragged{n} through 30 layers (cache-cold context)")
+        s_ms, dist = measure_ragged_stack30(seed, n_tok=n)
+        sbytes = sum(dist) * EXPERT_BYTES + len(dist) * ROUTER_BYTES
+        res["stack30"] = {"us_per_step": round(s_ms * 1e3, 2), "us_per_layer": round(s_ms * 1e3 / len(dist), 3),
+                          "layers": len(dist), "distinct_experts_per_layer": round(sum(dist) / len(dist), 1),
+                          "bytes_per_step": sbytes,
+                          "frac_of_hbm_peak": round(sbytes / (s_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                          "note": "30 layers of 428 MB each (12.9 GB), each with its own Zipf(1.1) bias and its "
+                                  "own N(0,1) tokens, one rvm_moe_forward per layer: the experts come from HBM, "
+                                  "not from the 256 MB last-level cache that the single-layer figure partly reads"}
+    return res
+
+
+def measure_token_latency(layer, seed: int, n_tok: int = 2000, per_graph: int = 100) -> dict:
+    """Per-token decode latency over n_tok fresh tokens: graphs of per_graph back-to-back decode calls
+    with an event recorded between tokens (event nodes in the graph), each graph replayed once to warm
+    and once timed. A token's latency is the time between the events around it; the router fallback
+    tokens (the certificate fails and the logits are folded in the reference's order) form the tail."""
+    import numpy as np
+
+    from rosevine_amd import hip, moe, synth
+
+    D = synth.D
+    x = hip.DevBuf.from_array(synth.tokens(seed + 500, n_tok))
+    out = hip.DevBuf(n_tok * D * 4)
+    ws = moe.Workspace(layer, 1)
+    ev = [hip.Event() for _ in range(per_graph + 1)]
+    lat, fb = [], []
+    nb = D * 4
+    try:
+        for g0 in range(0, n_tok, per_graph):
+            hip.Graph.begin()
+            try:
+                ev[0].record()
+                for i in range(per_graph):
+                    moe.decode(layer, x, out, ws, x_off=(g0 + i) * nb, out_off=(g0 + i) * nb)
+                    ev[i + 1].record()
+            finally:
+                g = hip.Graph.end()
+            g.launch()
+            hip.sync()
+            f0 = ws.fallbacks()
+            g.launch()
+            ev[-1].synchronize()
+            fb.append(ws.fallbacks() - f0)
+            lat.extend(ev[i].elapsed_ms(ev[i + 1]) * 1e3 for i in range(per_graph))
+            g.close()
+    except hip.DeviceError as e:
+        return {"error": f"event nodes in a captured graph: {e}"}
+    finally:
+        for b in (x, out, ws.buf):
+            b.close()
+    a = np.array(lat)
+    return {"tokens": len(a), "note": "each event node adds about 3 us to the token it closes (compare us_p50 "
+                                      "with the headline's graph time per token); the tail is the fallback tokens",
+            "us_p50": round(float(np.percentile(a, 50)), 2),
+            "us_p99": round(float(np.percentile(a, 99)), 2), "us_max": round(float(a.max()), 2),
+            "us_mean": round(float(a.mean()), 2), "router_fallbacks": int(sum(fb)),
+            "method": f"graphs of {per_graph} decode calls with an event node between tokens"}
+
+
+
 def other_workload(args) -> int:
     """The other configurations of the decode/prefill path, one JSON line each (not the headline)."""
     import numpy as np
@@ -233,48 +397,12 @@ def other_workload(args) -> int:
             "data": "synthetic (seeded Q4_0 experts, N(0,1) tokens, N(0,0.02) router)"}
     if args.workload in ("prefill512", "ragged32"):
         n = 512 if args.workload == "prefill512" else 32
-        bias = None if n == 512 else synth.zipf_bias(args.seed)
-        layer = moe.MoeLayer(E, K8, D, FF, synth.router_weights(args.seed, 0), bias)
-        layer.synth_weights(args.seed, synth.gate_up_stream(0), synth.down_stream(0))
-        xs = [hip.DevBuf.from_array(synth.tokens(args.seed + 200 + i, n)) for i in range(4)]
-        out = hip.DevBuf(n * D * 4)
-        ws = moe.Workspace(layer, n)
-        it = [0]
-
-        def run():
-            moe.forward(layer, xs[it[0] % 4], out, n, ws)
-            it[0] += 1
-
-        ms = _timed(run, max(5, args.steps // (100 if n == 512 else 10)), 3)
-        moe.forward(layer, xs[0], out, n, ws)
-        ids, _ = ws.selection(layer, n)
-        distinct = len(set(int(v) for v in ids.reshape(-1)))
-        nbytes = distinct * EXPERT_BYTES + ROUTER_BYTES
-        ops = n * K8 * ops_pair
-        stack = None
-        if n == 32 and not args.no_stack:
-            log("[bench] ragged32 through 30 layers (cache-cold context)")
-            s_ms, dist = measure_ragged_stack30(args.seed)
-            sbytes = sum(dist) * EXPERT_BYTES + len(dist) * ROUTER_BYTES
-            stack = {"us_per_step": round(s_ms * 1e3, 2), "us_per_layer": round(s_ms * 1e3 / len(dist), 3),
-                     "layers": len(dist), "distinct_experts_per_layer": round(sum(dist) / len(dist), 1),
-                     "bytes_per_step": sbytes,
-                     "frac_of_hbm_peak": round(sbytes / (s_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "note": "30 layers of 428 MB each (12.9 GB), each with its own Zipf(1.1) bias and its "
-                             "own 32 N(0,1) tokens, one rvm_moe_forward per layer: the experts come from HBM, "
-                             "not from the 256 MB last-level cache that the single-layer figure partly reads"}
-        line.update({"metric": f"MoE-layer forward tokens/s, {n} tokens", "value": round(n / (ms / 1e3), 1),
-                     "unit": "tokens/s", "steps": max(5, args.steps // (100 if n == 512 else 10)), "warmup": 3,
-                     "ms_per_step": round(ms, 6), "scaling": "weak",
-                     "config": {"workload": args.workload, "tokens": n, "distinct_experts": distinct,
-                                "routing": "iid" if bias is None else "Zipf(1.1) router bias"},
-                     "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms / 1e3) / 1e9, 1),
-                                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                  "frac": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
-                                  "bytes_per_step": nbytes, "int8_tops": round(ops / (ms / 1e3) / 1e12, 2),
-                                  "int8_frac_of_5000_tops": round(ops / (ms / 1e3) / 5.0e15, 5)}})
-        if stack:
-            line["stack30"] = stack
+        routing = "iid" if n == 512 else "zipf"
+        res = measure_batch(args.seed, n, routing, max(5, args.steps // (100 if n == 512 else 10)),
+                            stack=n == 32 and not args.no_stack)
+        line.update({"metric": f"MoE-layer forward tokens/s, {n} tokens", "value": res["tokens_per_s"],
+                     "unit": "tokens/s", "steps": res["steps"], "warmup": 3, "ms_per_step": res["us"] / 1e3,
+                     "scaling": "weak", "config": {"workload": args.workload, **res}})
     elif args.workload == "q4gemv":
         # the dense Q4_0 projections of one sliding-window layer of the reference model
         # (contract.rs:41-62) and its 262,144-row output head, one token, rvh_q4_mm
@@ -473,14 +601,15 @@ def other_workload(args) -> int:
     else:  # stack30
         L = 30
         n_tok = 40
-        ms, resident, calls = measure_stack30(args.seed, L, n_tok)
+        ms, resident, calls, spans = measure_stack30(args.seed, L, n_tok)
         nbytes = L * (K8 * EXPERT_BYTES + ROUTER_BYTES)
         line.update({"metric": "30-layer MoE stack decode tokens/s, batch 1", "value": round(1e3 / ms, 1),
                      "unit": "tokens/s", "steps": n_tok - 4, "warmup": 4, "ms_per_step": round(ms, 6),
                      "scaling": "weak",
                      "config": {"workload": "stack30", "layers": L, "resident_bytes": resident,
                                 "routing": "per-expert bias N(0,1)", "norm": "RMSNorm eps 1e-6 between layers",
-                                "us_per_layer": round(ms * 1e3 / L, 3), "device_calls_per_token": calls},
+                                "us_per_layer": round(ms * 1e3 / L, 3), "device_calls_per_token": calls,
+                                "spans": spans},
                      "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms / 1e3) / 1e9, 1),
                                   "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                   "frac": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -500,6 +629,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample time")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-stack", action="store_true", help="skip the 30-layer (cache-cold) context figure")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the per-token latency sample and the prefill-512 and ragged-32 lines")
     ap.add_argument("--attn-eager", action="store_true",
                     help="attn: launch the layers without graph capture (host-bound; for kernel tracing)")
     ap.add_argument("--attn-min-chunk", type=int, default=32,
@@ -591,17 +722,42 @@ def main() -> int:
     log(f"[bench] {ms_per_step * 1e3:.2f} us/token, {tok_s:.0f} tokens/s, {achieved:.0f} GB/s, "
         f"router fallbacks {fallbacks}/{K}")
 
+    latency = None
+    if not args.no_extras:
+        log("[bench] per-token latency over 2000 fresh tokens")
+        st2 = hip.Stream()
+        st2.use()
+        latency = measure_token_latency(layer, args.seed)
+        hip.Stream.use_default()
+        st2.close()
+        log(f"[bench] latency {latency}")
+    for b in (layer.gate_up, layer.down, layer.router, xd, out, ws.buf):
+        b.close()
+
     stack = None
     if not args.no_stack:
         log("[bench] 30-layer stack (cache-cold context)")
-        s30, resident, calls = measure_stack30(args.seed)
+        s30, resident, calls, spans = measure_stack30(args.seed)
         stack = {"us_per_token": round(s30 * 1e3, 2), "us_per_layer": round(s30 * 1e3 / 30, 3),
                  "layers": 30, "resident_bytes": resident, "executor": "rvm_session_eval",
-                 "device_calls_per_token": calls,
+                 "device_calls_per_token": calls, "spans": spans,
                  "frac_of_hbm_peak": round(30 * bytes_tok / (s30 / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
                  "note": "config 3: single-token decode through 30 layers (router bias, RMSNorm between "
                          "layers), 12.9 GB of experts, none of it held in the 256 MB last-level cache"}
         log(f"[bench] stack30: {stack['us_per_layer']} us per layer")
+
+    batches = None
+    if not args.no_extras:
+        st3 = hip.Stream()
+        st3.use()
+        batches = {}
+        for name, n, routing, steps in [("prefill512", 512, "iid", 20), ("prefill512_skewed", 512, "skewed", 20),
+                                        ("ragged32", 32, "zipf", 100)]:
+            log(f"[bench] {name}")
+            batches[name] = measure_batch(args.seed, n, routing, steps, stack=n == 32 and not args.no_stack)
+            log(f"[bench] {name}: {batches[name]['us']} us")
+        hip.Stream.use_default()
+        st3.close()
 
     cpu = None
     if not args.no_cpu:
@@ -633,9 +789,12 @@ def main() -> int:
                      "cache_note": "one layer's 428 MB of experts against MI355X's 256 MB last-level cache: "
                                    "part of each token's expert bytes hit that cache; stack30 reads 12.9 GB "
                                    "and is the cache-cold figure"},
+        "latency": latency,
         "stack30": stack,
         "cpu_baseline": cpu,
     }
+    if batches:
+        line.update(batches)
     print(json.dumps(line), flush=True)
     return 0
 

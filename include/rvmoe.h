@@ -238,9 +238,10 @@ int rvm_moe_forward(const rvm_layer *layer, const float *x, float *out, int n_to
 
 /* Device calls issued by the calling thread through this library since the last reset (the
  * reference's per-thread Counters of runtime/src/hip.rs:167-187): kernel launches, host-to-device,
- * device-to-host and device-to-device copies, host synchronisations (rvh_sync, rvh_event_sync, and
- * the synchronising rvh_upload / rvh_download), and graph launches. Inside a graph capture the
- * launches counted are the captured ones. */
+ * device-to-host and device-to-device copies, explicit host synchronisations (rvh_sync and
+ * rvh_event_sync; as in the reference, rvh_upload and rvh_download count as copies only, though they
+ * wait for their copy), and graph launches. Inside a graph capture the launches counted are the
+ * captured ones. */
 typedef struct rvm_counters {
     uint64_t launches, h2d, d2h, d2d, syncs, graphs;
 } rvm_counters;
@@ -270,6 +271,21 @@ int rvm_session_destroy(rvm_session *session);
  * rvm_moe_* call (3 for one token), no transfer and no host synchronisation, so the call can be
  * captured in one graph. flags: 0 or RVM_EXACT_SELECT. */
 int rvm_session_eval(rvm_session *session, const float *x, float *out, int n_tok, int flags);
+/* Layers [l0, l1) of the same evaluation, so that a caller can stop between ranges: the reference's
+ * HipSession::eval polls its cancel closure before every layer (runtime/src/hip_exec.rs:645-655); a
+ * caller polls it between ranges instead. A range from l0 = 0 starts an evaluation and reads x; any
+ * other range must start where the previous range of this session ended, with the same n_tok (else
+ * hipErrorInvalidValue); the range that ends at the last layer writes out (x and out may be NULL
+ * where they are not read or written). The ranges of one evaluation issue exactly the kernels of
+ * rvm_session_eval, so the result is the same bit for bit. A caller that stops early starts the
+ * next evaluation from l0 = 0. */
+int rvm_session_eval_range(rvm_session *session, const float *x, float *out, int n_tok, int flags, int l0, int l1);
+/* Span events (instrumentation, the device-event mode of runtime/src/instr.rs): events[2l] is recorded
+ * on the current stream before layer l's router work, events[2l + 1] once that router work is issued,
+ * before its expert work, and events[2 n_layers] after the last layer; n_events = 2 n_layers + 1,
+ * each from rvh_event_create. NULL turns the probe off. The spans "router" (2l to 2l + 1) and
+ * "gpu_experts" (2l + 1 to 2l + 2) are then read with rvh_event_elapsed; there is no "exp_meta". */
+int rvm_session_probe(rvm_session *session, void *const *events, int n_events);
 /* The session's workspace (for rvm_workspace_selection / rvm_workspace_fallbacks of its last layer). */
 int rvm_session_workspace(const rvm_session *session, const void **ws);
 

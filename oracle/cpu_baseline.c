@@ -14,6 +14,7 @@
 #include <stdatomic.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include "moe_oracle.h"
 
@@ -55,7 +56,19 @@ struct cpb_pool {
     uint32_t *order, *pos_of, *gs;
     seg_t *segs;
     size_t *starts;
+    /* wall time of the expert part of every cpb_moe_layer call so far (plan, quantisation, the two
+       pooled GEMV segments, GeGLU, combine: what the reference's CPU expert span covers, without the
+       router and selection that run before it on the caller thread) */
+    uint64_t expert_ns;
 };
+
+static uint64_t now_ns(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (uint64_t)ts.tv_sec * 1000000000ull + (uint64_t)ts.tv_nsec;
+}
+
+uint64_t cpb_expert_ns(const cpb_pool *p) { return p ? p->expert_ns : 0; }
 
 static int g_avx2 = -1;
 
@@ -264,6 +277,7 @@ int cpb_moe_layer(cpb_pool *p, const float *w_r, const float *bias, const uint8_
     orc_select_experts(p->logits, n_tok, n_exp, used, ids, weights);
     for (size_t i = 0; i < pairs; ++i)
         if (ids[i] >= n_exp || !gate_up[ids[i]] || !down[ids[i]]) return -1;
+    const uint64_t t0 = now_ns();
     orc_moe_plan(ids, pairs, n_exp, p->order, p->pos_of, p->gs);
     size_t xq_bytes = d / QK * Q8_BLOCK, hq_bytes = ff / QK * Q8_BLOCK;
     /* gather + caller-thread quantisation of each segment row */
@@ -289,5 +303,6 @@ int cpb_moe_layer(cpb_pool *p, const float *w_r, const float *bias, const uint8_
                 for (size_t i = 0; i < d; ++i) o[i] += yy[i] * ds * wt;
         }
     }
+    p->expert_ns += now_ns() - t0;
     return 0;
 }

@@ -108,6 +108,10 @@ void cpb_destroy(cpb_pool *pool);
 int cpb_threads(const cpb_pool *pool);
 /* 1 when the AVX2+FMA kernel runs, 0 for the scalar kernel. */
 int cpb_uses_avx2(void);
+/* Nanoseconds spent in the expert part (plan, quantisation, the pooled GEMV segments, GeGLU and
+ * combine) of every cpb_moe_layer call on this pool so far; the router and selection before it are
+ * not included. */
+uint64_t cpb_expert_ns(const cpb_pool *pool);
 /* One MoE layer for n_tok tokens on the pool (router and selection on the caller thread, as
  * runtime/src/exec.rs:456-475). Same arguments as orc_moe_layer. */
 int cpb_moe_layer(cpb_pool *pool, const float *w_r, const float *bias, const uint8_t *const *gate_up,

@@ -107,6 +107,7 @@ def _declare(L):
         "cpb_destroy": (None, [vp]),
         "cpb_threads": (i32, [vp]),
         "cpb_uses_avx2": (i32, []),
+        "cpb_expert_ns": (C.c_uint64, [vp]),
         "cpb_moe_layer": (i32, [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
@@ -368,6 +369,10 @@ class CpuBaseline:
 
     def __del__(self):
         self.close()
+
+    def expert_seconds(self) -> float:
+        """Wall time of the expert part (after router and selection) of every layer call so far."""
+        return lib().cpb_expert_ns(self.pool) * 1e-9
 
     def prepare(self, gate_up, down, n_exp):
         """Bind expert weight pointers once (they stay alive with this object)."""

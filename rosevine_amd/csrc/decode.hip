@@ -304,7 +304,7 @@ int moe_decode(const rvm_layer *L, const float *x, float *out, int flags, const 
     int32_t *ids = (int32_t *)(w + lay.ids);
     float *wts = (float *)(w + lay.wts);
     int rc = launch_router(L, x, 1, flags, xf, w, lay, ids, wts, nullptr, false);
-    if (rc) return rc;
+    if (rc || (rc = span_router_done())) return rc;
 
     const int Tg = 2 * L->ff / 64;
     const size_t gu_entries = (size_t)L->n_exp * 2 * L->ff * (L->d / QK);

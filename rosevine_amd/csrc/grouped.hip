@@ -685,7 +685,7 @@ int moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int f
     float *wts = (float *)(w + lay.wts);
     int32_t *pos_of = (int32_t *)(w + lay.pos_of);
     int rc = launch_router(L, x, n_tok, flags, xf, w, lay, ids, wts, nullptr, true);
-    if (rc) return rc;
+    if (rc || (rc = span_router_done())) return rc;
     constexpr int GU_MT = 2, DN_MT = 3;  // m-tiles per tile of the two MFMA kernels
     const int cap = tile_pairs(L, n_tok);
     const bool quad = cap == QUAD;

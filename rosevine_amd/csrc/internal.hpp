@@ -340,6 +340,14 @@ inline XForm xform_of_flags(int flags, float eps) {
 // The router and expert inputs differ (a gain or a post factor is set).
 __host__ __device__ inline bool xform_split(const XForm &xf) { return xf.rg || xf.eg || xf.rpost != 1.0f; }
 
+// Span instrumentation of the session executor: when set, the layer call issued next records e on
+// the current stream once its router work is issued (span_router_done), before its expert work.
+void span_mark_after_router(hipEvent_t e);
+int span_router_done();
+// Records e on the current stream (an event node of the graph under capture); 0 or the error,
+// which is also cleared from the thread's last error.
+int record_event(hipEvent_t e);
+
 // Kernel launchers shared across translation units.
 // k_router (logit statistics and the Q8_0 input), then k_select unless select is false.
 int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, const XForm &xf, uint8_t *ws,

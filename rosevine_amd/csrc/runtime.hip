@@ -12,6 +12,33 @@ static thread_local rvm_counters g_count{};
 
 hipStream_t cur_stream() { return g_stream; }
 
+static thread_local hipEvent_t g_span = nullptr;
+
+// A failed runtime call leaves its code as the thread's last error, which the next launch check
+// (hipGetLastError in launched()) would report as its own: return the code and clear it.
+int api_status(hipError_t e) {
+    if (e != hipSuccess) (void)hipGetLastError();
+    return (int)e;
+}
+
+// Records e on the current stream; under stream capture as an event node of the graph (the
+// external-event form, whose timestamps hipEventElapsedTime reads after a replay).
+int record_event(hipEvent_t e) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (int rc = api_status(hipStreamIsCapturing(g_stream, &st))) return rc;
+    const unsigned flags = st == hipStreamCaptureStatusActive ? hipEventRecordExternal : 0u;
+    return api_status(hipEventRecordWithFlags(e, g_stream, flags));
+}
+
+void span_mark_after_router(hipEvent_t e) { g_span = e; }
+
+int span_router_done() {
+    if (!g_span) return 0;
+    const hipEvent_t e = g_span;
+    g_span = nullptr;
+    return record_event(e);
+}
+
 int launched() {
     ++g_count.launches;
     return (int)hipGetLastError();
@@ -165,8 +192,7 @@ int rvh_free(void *ptr) { return ptr ? (int)hipFree(ptr) : 0; }
 
 int rvh_upload(void *dst, const void *src, size_t bytes) {
     RVM_CHECK(dst && src);
-    ++g_count.h2d;
-    ++g_count.syncs;
+    ++g_count.h2d;  // a transfer, not a counted sync (the reference counts only explicit syncs)
     RVM_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, cur_stream()));
     return (int)hipStreamSynchronize(cur_stream());
 }
@@ -174,7 +200,6 @@ int rvh_upload(void *dst, const void *src, size_t bytes) {
 int rvh_download(void *dst, const void *src, size_t bytes) {
     RVM_CHECK(dst && src);
     ++g_count.d2h;
-    ++g_count.syncs;
     RVM_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, cur_stream()));
     return (int)hipStreamSynchronize(cur_stream());
 }
@@ -222,7 +247,7 @@ int rvh_event_destroy(void *ev) { return ev ? (int)hipEventDestroy((hipEvent_t)e
 
 int rvh_event_record(void *ev) {
     RVM_CHECK(ev);
-    return (int)hipEventRecord((hipEvent_t)ev, cur_stream());
+    return record_event((hipEvent_t)ev);
 }
 
 int rvh_event_sync(void *ev) {
@@ -253,18 +278,18 @@ int rvm_stream_destroy(void *stream) { return stream ? (int)hipStreamDestroy((hi
 
 int rvm_graph_begin(void) {
     RVM_CHECK(cur_stream() != nullptr);
-    return (int)hipStreamBeginCapture(cur_stream(), hipStreamCaptureModeThreadLocal);
+    return api_status(hipStreamBeginCapture(cur_stream(), hipStreamCaptureModeThreadLocal));
 }
 
 int rvm_graph_end(void **graph_exec) {
     RVM_CHECK(graph_exec && cur_stream() != nullptr);
     *graph_exec = nullptr;
     hipGraph_t g = nullptr;
-    RVM_TRY(hipStreamEndCapture(cur_stream(), &g));
+    if (int rc = api_status(hipStreamEndCapture(cur_stream(), &g))) return rc;
     hipGraphExec_t ex = nullptr;
     hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
-    if (e != hipSuccess) return (int)e;
+    if (e != hipSuccess) return api_status(e);
     *graph_exec = (void *)ex;
     return 0;
 }
@@ -272,7 +297,7 @@ int rvm_graph_end(void **graph_exec) {
 int rvm_graph_launch(void *graph_exec) {
     RVM_CHECK(graph_exec);
     ++g_count.graphs;
-    return (int)hipGraphLaunch((hipGraphExec_t)graph_exec, cur_stream());
+    return api_status(hipGraphLaunch((hipGraphExec_t)graph_exec, cur_stream()));
 }
 
 int rvm_graph_destroy(void *graph_exec) {

@@ -24,6 +24,12 @@ struct rvm_session {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     float *buf[2] = {nullptr, nullptr};
+    // Range evaluation: the layer the next range must start at (0: a new evaluation) and the token
+    // count of the evaluation in progress.
+    int next = 0, n_tok = 0;
+    // Span events (instrumentation, off when empty): 2 per layer, recorded on the current stream
+    // before the layer's router work and before its expert work, then one after the last layer.
+    std::vector<hipEvent_t> probe;
 };
 
 namespace {
@@ -86,14 +92,25 @@ int rvm_session_workspace(const rvm_session *s, const void **ws) {
     return 0;
 }
 
-int rvm_session_eval(rvm_session *s, const float *x, float *out, int n_tok, int flags) {
-    RVM_CHECK(s && x && out && n_tok > 0 && n_tok <= s->max_tokens);
+int rvm_session_eval_range(rvm_session *s, const float *x, float *out, int n_tok, int flags, int l0, int l1) {
+    RVM_CHECK(s && n_tok > 0 && n_tok <= s->max_tokens);
     RVM_CHECK((flags & ~RVM_EXACT_SELECT) == 0);
     const int n = (int)s->layers.size();
-    for (int l = 0; l < n; ++l) {
+    RVM_CHECK(l0 >= 0 && l0 < l1 && l1 <= n);
+    // A range continues the evaluation in progress: it starts where the previous range ended, with
+    // the same tokens; only a range from layer 0 starts a new one (and needs x), and only the range
+    // that ends at the last layer writes out.
+    RVM_CHECK(l0 == 0 ? x != nullptr : (l0 == s->next && n_tok == s->n_tok));
+    RVM_CHECK(l1 < n || out != nullptr);
+    const bool probe = !s->probe.empty();
+    for (int l = l0; l < l1; ++l) {
         const float *in = l == 0 ? x : s->buf[(l - 1) & 1];
         float *dst = l == n - 1 ? out : s->buf[l & 1];
         const rvm_layer *L = &s->layers[l];
+        if (probe) {
+            if (int rc = record_event(s->probe[2 * l])) return rc;
+            span_mark_after_router(s->probe[2 * l + 1]);
+        }
         int rc;
         if (!s->norms.empty()) {
             const rvm_block_norms &nm = s->norms[l];
@@ -103,8 +120,33 @@ int rvm_session_eval(rvm_session *s, const float *x, float *out, int n_tok, int 
             const int f = flags | (l > 0 ? RVM_PRE_NORM : 0);
             rc = moe_forward(L, in, dst, n_tok, f, xform_of_flags(f, s->eps), s->ws, s->ws_bytes);
         }
-        if (rc) return rc;
+        span_mark_after_router(nullptr);
+        if (rc) {
+            s->next = 0;
+            return rc;
+        }
     }
+    if (probe && l1 == n)
+        if (int rc = record_event(s->probe[2 * n])) return rc;
+    s->next = l1 == n ? 0 : l1;
+    s->n_tok = n_tok;
+    return 0;
+}
+
+int rvm_session_eval(rvm_session *s, const float *x, float *out, int n_tok, int flags) {
+    RVM_CHECK(s && x && out);
+    return rvm_session_eval_range(s, x, out, n_tok, flags, 0, (int)s->layers.size());
+}
+
+int rvm_session_probe(rvm_session *s, void *const *events, int n_events) {
+    RVM_CHECK(s);
+    if (!events) {
+        s->probe.clear();
+        return 0;
+    }
+    RVM_CHECK(n_events == 2 * (int)s->layers.size() + 1);
+    for (int i = 0; i < n_events; ++i) RVM_CHECK(events[i] != nullptr);
+    s->probe.assign((hipEvent_t const *)events, (hipEvent_t const *)events + n_events);
     return 0;
 }
 

@@ -132,6 +132,8 @@ SIGNATURES = {
     "rvm_session_create": (_i, [_vp, _i, _vp, _i, _f, C.POINTER(_vp)]),
     "rvm_session_destroy": (_i, [_vp]),
     "rvm_session_eval": (_i, [_vp, _vp, _vp, _i, _i]),
+    "rvm_session_eval_range": (_i, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "rvm_session_probe": (_i, [_vp, _vp, _i]),
     "rvm_session_workspace": (_i, [_vp, C.POINTER(_vp)]),
     "rvm_gguf_open": (_i, [_vp, _sz, C.POINTER(_vp)]),
     "rvm_gguf_close": (_i, [_vp]),

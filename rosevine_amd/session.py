@@ -39,6 +39,39 @@ class Session:
             raise hip.BoundsError("session sized for fewer tokens")
         nb = n_tok * self.d * 4
         check(lib().rvm_session_eval(self.handle, x.at(x_off, nb), out.at(out_off, nb), n_tok, flags))
+        self._next = 0
+
+    def eval_range(self, x: DevBuf | None, out: DevBuf | None, n_tok: int, l0: int, l1: int, flags: int = 0,
+                   x_off: int = 0, out_off: int = 0) -> None:
+        """Layers [l0, l1) of one evaluation (rvm_session_eval_range): a caller polls its cancel flag
+        between ranges, as the reference's HipSession::eval does before every layer
+        (runtime/src/hip_exec.rs:645-655). The range checks are the library's, made here first."""
+        n = len(self.layers)
+        if not (0 <= l0 < l1 <= n):
+            raise hip.BoundsError(f"layer range [{l0}, {l1}) outside a {n}-layer session")
+        if not 0 < n_tok <= self.max_tokens:
+            raise hip.BoundsError("session sized for fewer tokens")
+        if l0 > 0 and (l0 != getattr(self, "_next", 0) or n_tok != getattr(self, "_ntok", 0)):
+            raise hip.BoundsError(f"range from layer {l0} does not continue the evaluation in progress")
+        nb = n_tok * self.d * 4
+        if l0 == 0 and x is None:
+            raise hip.BoundsError("a range from layer 0 reads x")
+        if l1 == n and out is None:
+            raise hip.BoundsError("the range that ends at the last layer writes out")
+        xp = x.at(x_off, nb) if l0 == 0 else None
+        op = out.at(out_off, nb) if l1 == n else None
+        check(lib().rvm_session_eval_range(self.handle, xp, op, n_tok, flags, l0, l1))
+        self._next, self._ntok = (0 if l1 == n else l1), n_tok
+
+    def probe(self, events: list | None) -> None:
+        """Span events (rvm_session_probe): 2 per layer and one at the end, or None to stop."""
+        if events is None:
+            check(lib().rvm_session_probe(self.handle, None, 0))
+            self._probe = None
+            return
+        arr = (C.c_void_p * len(events))(*[e.ptr for e in events])
+        check(lib().rvm_session_probe(self.handle, arr, len(events)))
+        self._probe = (arr, events)  # kept alive while the library holds them
 
     def selection(self, n_tok: int):
         """ids and weights of the last layer of the last evaluation (synchronises)."""

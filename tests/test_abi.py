@@ -104,3 +104,42 @@ def test_q4_mm_n_rejects_bad_counts_before_any_call(rvlib):
     assert rvlib.rvm_q4_mm_n(2, odd, rows, y, C.c_void_p(0x3000), 2816, 1) == 1
     bad_rows = (C.c_int * 2)(64, 0)
     assert rvlib.rvm_q4_mm_n(2, w, bad_rows, y, C.c_void_p(0x3000), 2816, 1) == 1
+
+
+def test_session_layer_ranges_are_refused_before_any_call(rvlib):
+    """rvm_session_eval_range's contract (the cancellation points of runtime/src/hip_exec.rs:645-655):
+    a range lies inside the stack, a range after layer 0 continues the evaluation in progress with the
+    same tokens, layer 0 needs x and the last layer needs out. The Python host side makes the library's
+    checks first, so none of these reaches the device; the library refuses a null session itself."""
+    import pytest
+
+    from rosevine_amd import hip, session
+
+    class Buf(hip.DevBuf):
+        def __init__(self, n):  # no allocation: only the range logic is exercised
+            self.ptr, self.nbytes = 0x1000, n
+
+        def close(self):
+            self.ptr = None
+
+    s = object.__new__(session.Session)
+    s.layers, s.max_tokens, s.d, s.handle = [object()] * 4, 2, 256, None
+    x, out = Buf(2 * 256 * 4), Buf(2 * 256 * 4)
+    for l0, l1 in [(-1, 2), (2, 2), (3, 1), (0, 5), (4, 4)]:
+        with pytest.raises(hip.BoundsError):
+            s.eval_range(x, out, 1, l0, l1)
+    with pytest.raises(hip.BoundsError):
+        s.eval_range(x, out, 3, 0, 2)  # more tokens than the session holds
+    with pytest.raises(hip.BoundsError):
+        s.eval_range(None, out, 1, 0, 2)  # layer 0 reads x
+    with pytest.raises(hip.BoundsError):
+        s.eval_range(x, None, 1, 0, 4)  # the last layer writes out
+    with pytest.raises(hip.BoundsError):
+        s.eval_range(x, out, 1, 2, 4)  # no evaluation in progress: must start at layer 0
+    s._next, s._ntok = 2, 1
+    with pytest.raises(hip.BoundsError):
+        s.eval_range(x, out, 1, 3, 4)  # does not continue at layer 2
+    with pytest.raises(hip.BoundsError):
+        s.eval_range(x, out, 2, 2, 4)  # other tokens than the evaluation in progress
+    assert rvlib.rvm_session_eval_range(None, None, None, 1, 0, 0, 1) == 1  # hipErrorInvalidValue
+    assert rvlib.rvm_session_probe(None, None, 0) == 1

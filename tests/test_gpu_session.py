@@ -136,3 +136,40 @@ def test_session_with_block_norms(gpu, orc):
             assert_close(nxt.download(np.float32, D), want, "layer 0")
         cur = nxt
     assert np.array_equal(cur.download(np.float32, D), got)
+
+
+def test_session_layer_ranges_equal_the_whole_evaluation(gpu):
+    """rvm_session_eval_range: the layers evaluated in ranges, with a caller's cancel check between
+    ranges (runtime/src/hip_exec.rs:645-655), give the whole evaluation's bits, for a decode token and
+    for a batch; an evaluation stopped after a range leaves the next one, from layer 0, unaffected;
+    the span probe's events bracket each layer's router and expert work."""
+    keys = [get_layer(l, bias=True) for l in range(4)]
+    s = session.Session([k[0] for k in keys], max_tokens=8, eps=1e-6)
+    for n in (1, 5):
+        print(f"[session] layer ranges, {n} tokens", flush=True)
+        x = synth.tokens(SEED + 303 + n, n)
+        xd, whole, ranged = dev(x), DevBuf(n * D * 4), DevBuf(n * D * 4)
+        s.eval(xd, whole, n)
+        want = whole.download(np.float32, n * D)
+        s.eval_range(xd, None, n, 0, 2)  # cancelled after two layers
+        hip.reset_counters()
+        for l0, l1 in [(0, 1), (1, 3), (3, 4)]:
+            s.eval_range(xd if l0 == 0 else None, ranged if l1 == 4 else None, n, l0, l1)
+        assert hip.counters()["syncs"] == 0
+        assert np.array_equal(ranged.download(np.float32, n * D), want), n
+        with pytest.raises(hip.BoundsError):
+            s.eval_range(None, ranged, n, 2, 4)  # the evaluation ended: a new one starts at layer 0
+    # span events: router, then experts, per layer
+    ev = [hip.Event() for _ in range(2 * len(keys) + 1)]
+    s.probe(ev)
+    x = synth.tokens(SEED + 310, 1)
+    xd, out = dev(x), DevBuf(D * 4)
+    s.eval(xd, out, 1)
+    ev[-1].synchronize()
+    s.probe(None)
+    probed = out.download(np.float32, D)
+    for l in range(len(keys)):
+        router, experts = ev[2 * l].elapsed_ms(ev[2 * l + 1]), ev[2 * l + 1].elapsed_ms(ev[2 * l + 2])
+        assert router >= 0.0 and experts > 0.0, (l, router, experts)
+    s.eval(xd, out, 1)  # the probe is off again; the events changed nothing
+    assert np.array_equal(out.download(np.float32, D), probed)
