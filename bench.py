@@ -158,6 +158,7 @@ def measure_stack30(seed: int, n_layers: int = 30, n_tok: int = 40):
     timed = [capture(t, min(GRAPH_TOKENS, n_tok - t)) for t in range(4, n_tok, GRAPH_TOKENS)]
     warm.launch()
     hip.sync()
+    fb0 = s.fallbacks()
     e0, e1 = hip.Event(), hip.Event()
     e0.record()
     for g in timed:
@@ -165,9 +166,11 @@ def measure_stack30(seed: int, n_layers: int = 30, n_tok: int = 40):
     e1.record()
     e1.synchronize()
     ms = e0.elapsed_ms(e1) / (n_tok - 4)
+    calls["router_fallbacks"] = s.fallbacks() - fb0
+    calls["selections"] = (n_tok - 4) * n_layers
     for g in [warm] + timed:
         g.close()
-    spans = stack_spans(s, x, out, n_layers, n_tok)
+    spans = stack_spans(s, x, out, n_layers, n_tok, ms * 1e3 / n_layers)
     s.close()
     hip.Stream.use_default()
     stream.close()
@@ -179,7 +182,7 @@ def measure_stack30(seed: int, n_layers: int = 30, n_tok: int = 40):
     return ms, resident, calls, spans
 
 
-def stack_spans(s, x, out, n_layers: int, n_tok: int) -> dict:
+def stack_spans(s, x, out, n_layers: int, n_tok: int, unprobed_us: float) -> dict:
     """Per-layer device time of the reference's decode spans (runtime/src/instr.rs:98-132) through the
     session's probe events: "router" from a layer's start to its router work issued, "gpu_experts" from
     there to the layer's end, "exp_meta" 0 (no dispatch metadata is uploaded). One token per graph,
@@ -212,11 +215,16 @@ def stack_spans(s, x, out, n_layers: int, n_tok: int) -> dict:
         return {"error": f"probe events in a captured graph: {err}"}
     finally:
         s.probe(None)
-    return {"router_us_per_layer": round(sum(router) / len(router), 3),
-            "gpu_experts_us_per_layer": round(sum(experts) / len(experts), 3), "exp_meta_us_per_layer": 0.0,
-            "probed_us_per_layer": round(sum(total) / len(total), 3),
-            "note": "each event node adds about 3 us to the span it closes, so the probed layer is longer than the "
-                    "unprobed one (us_per_layer); the spans show the split, not the unprobed times",
+    r_us, e_us, p_us = sum(router) / len(router), sum(experts) / len(experts), sum(total) / len(total)
+    ev_us = (p_us - unprobed_us) / 2  # each layer's two event nodes lengthen it by their own cost
+    return {"router_us_per_layer": round(r_us - ev_us, 3), "gpu_experts_us_per_layer": round(e_us - ev_us, 3),
+            "exp_meta_us_per_layer": 0.0,
+            "probed": {"router_us_per_layer": round(r_us, 3), "gpu_experts_us_per_layer": round(e_us, 3),
+                       "us_per_layer": round(p_us, 3), "event_node_us": round(ev_us, 3)},
+            "note": "each event node lengthens the span it closes; the spans are the probed ones less that cost, "
+                    "(probed - unprobed layer time) / 2 per node, so that they add up to the unprobed layer; "
+                    "router = k_router and its launch gap, gpu_experts = gate/up (with the selection) and down "
+                    "fold, exp_meta = 0 (no dispatch metadata is uploaded)",
             "method": "rvm_session_probe events as graph nodes, one token per graph, mean of 8 tokens"}
 
 

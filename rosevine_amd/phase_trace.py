@@ -99,11 +99,54 @@ def table(s: np.ndarray, E: int, K: int, D: int, FF: int) -> None:
         print(f"| {label} | {len(v)} | {us.min():.2f} | {np.median(us):.2f} | {us.max():.2f} |")
 
 
+def stack_trace(seed: int, n: int) -> None:
+    """A layer in the middle of a decode stack (router bias, RMSNorm between layers, cold weights): a
+    3-layer session evaluated over layers 0 and 1 only (rvm_session_eval_range), so that the stamps
+    left are layer 1's, whose router reads layer 0's output. The graph time is per token (two
+    layers)."""
+    from . import session
+
+    E, K, D, FF = synth.N_EXP, synth.TOP_K, synth.D, synth.FF
+    layers = []
+    for l in range(3):
+        L = moe.MoeLayer(E, K, D, FF, synth.router_weights(seed, l), synth.router_bias(seed, l))
+        L.synth_weights(seed, synth.gate_up_stream(l), synth.down_stream(l))
+        layers.append(L)
+    s = session.Session(layers, max_tokens=1, eps=1e-6)
+    x = hip.DevBuf.from_array(synth.tokens(seed + 300, n))
+    hip.sync()
+    st = hip.Stream()
+    st.use()
+    hip.Graph.begin()
+    for t in range(n):
+        s.eval_range(x, None, 1, 0, 2, x_off=t * D * 4)
+    g = hip.Graph.end()
+    for _ in range(3):
+        g.launch()
+    hip.sync()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record()
+    g.launch()
+    e1.record()
+    e1.synchronize()
+    us_tok = e0.elapsed_ms(e1) * 1e3 / n
+    v = read_stamps()
+    g.close()
+    hip.Stream.use_default()
+    st.close()
+    print(f"\nlayer 1 of a decode stack (last of a {n}-token graph; graph {us_tok:.2f} us per token of 2 layers)")
+    table(v, E, K, D, FF)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--tokens", type=int, default=64, help="decode calls per captured graph")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--stack", action="store_true", help="a fused layer in the middle of a decode stack")
     args = ap.parse_args()
+    if args.stack:
+        stack_trace(args.seed, args.tokens)
+        return 0
     E, K, D, FF = synth.N_EXP, synth.TOP_K, synth.D, synth.FF
     L = moe.MoeLayer(E, K, D, FF, synth.router_weights(args.seed, 0))
     L.synth_weights(args.seed, synth.gate_up_stream(0), synth.down_stream(0))

@@ -73,6 +73,15 @@ class Session:
         check(lib().rvm_session_probe(self.handle, arr, len(events)))
         self._probe = (arr, events)  # kept alive while the library holds them
 
+    def fallbacks(self) -> int:
+        """Router selections of all layers so far whose certificate failed (rvm_workspace_fallbacks;
+        synchronises)."""
+        ws = C.c_void_p()
+        check(lib().rvm_session_workspace(self.handle, C.byref(ws)))
+        n = C.c_uint32()
+        check(lib().rvm_workspace_fallbacks(ws.value, C.byref(n)))
+        return n.value
+
     def selection(self, n_tok: int):
         """ids and weights of the last layer of the last evaluation (synchronises)."""
         ws = C.c_void_p()
