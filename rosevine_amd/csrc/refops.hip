@@ -1,14 +1,16 @@
-// SPDX-License-Identifier: GPL-3.0-only
-// refops.hip - the reference's per-operation expert-path kernels with their rvhip.h signatures
+// refops.hip - the reference's per-operation expert-path operators with their rvhip.h signatures
 // (runtime/hip/rvhip.h:42-80), written for wave64: a caller of the reference ABI (its
 // runtime/src/hip_exec.rs:780-843 dispatch) can bind these symbols unchanged. The fused
 // rvm_moe_* entry points are the fast path; these keep the per-operation contract.
 //
-// Attribution: k_rms_norm, k_geglu_split, k_gather_rows and k_moe_combine follow the reference's
-// kernels of the same operators (Rowanjgc/Rosevine runtime/hip/rvhip.hip:75-90 and 401-436,
-// GPL-3.0-only) statement for statement where the bitwise contract of those operators
-// (runtime/tests/hip_ops.rs:421-439) fixes every operation; this file is therefore distributed
-// under the reference's licence. k_f32_mm and k_q4_mm are this project's own designs.
+// The element-wise operators (rms_norm, geglu_split, gather_rows, moe_combine) compute every
+// element with the operations, and in the order, that the reference's operator contract fixes
+// (runtime/tests/hip_ops.rs:402-439: rms_norm and geglu_split within a relative 1e-6, gather_rows
+// and moe_combine bit for bit; runtime/src/ops.rs:131-149 and runtime/src/exec.rs:626-638 state
+// the arithmetic); their kernels are this library's: 16-byte columns wherever the rows allow,
+// a flat grid of (row, column chunk) workgroups, and per-row scalars read once per workgroup.
+#include <initializer_list>
+
 #include "internal.hpp"
 
 namespace rvm {
@@ -19,28 +21,73 @@ __device__ __forceinline__ float wave_sum_f(float v) {
     return v;
 }
 
-// out = ((x * 1/sqrt(mean(x^2) + eps)) * post) * weight, f64 sum of squares
-// (runtime/hip/rvhip.hip:75-90 semantics; runtime/src/ops.rs:131-139).
-__global__ __launch_bounds__(256) void k_rms_norm(const float *x, float *out, const float *__restrict__ w,
-                                                  int width, float eps, float post) {
-    __shared__ double sh[4];
+// ---- Element-wise operators: V floats per thread and column chunk (V = 4 where every row
+// starts 16-byte aligned and the width is a multiple of 4, else 1) ----
+template <int V>
+struct Cols;
+template <>
+struct Cols<4> {
+    float v[4];
+    __device__ __forceinline__ void load(const float *p) {
+        const float4 q = *(const float4 *)p;
+        v[0] = q.x;
+        v[1] = q.y;
+        v[2] = q.z;
+        v[3] = q.w;
+    }
+    __device__ __forceinline__ void store(float *p) const { *(float4 *)p = make_float4(v[0], v[1], v[2], v[3]); }
+};
+template <>
+struct Cols<1> {
+    float v[1];
+    __device__ __forceinline__ void load(const float *p) { v[0] = *p; }
+    __device__ __forceinline__ void store(float *p) const { *p = v[0]; }
+};
+// The rows' 16-byte columns are usable: base pointers 16-byte aligned and width a multiple of 4.
+inline bool cols4(int width, std::initializer_list<const void *> ptrs) {
+    if (width % 4) return false;
+    for (const void *p : ptrs)
+        if (p && ((uintptr_t)p & 15)) return false;
+    return true;
+}
+constexpr int EW_THREADS = 256;
+
+// rms_norm of row blockIdx.x: s = 1 / sqrt(mean(x^2) + eps) with the sum of squares in f64 (each
+// wave's partial sums joined in a fixed order), then ((x * s) * post) * w[i] per element, each
+// product rounded (runtime/src/ops.rs:131-139; the post factor and the weight only when set).
+// x may be out: every element is read before the barrier that precedes the first store.
+template <int V>
+__global__ __launch_bounds__(EW_THREADS) void k_rms_norm(const float *x, float *out, const float *__restrict__ w,
+                                                         int width, float eps, float post) {
+    __shared__ double part[EW_THREADS / 64];
     const float *xr = x + (size_t)blockIdx.x * width;
     float *o = out + (size_t)blockIdx.x * width;
     double s = 0.0;
-    for (int i = threadIdx.x; i < width; i += 256) s += (double)xr[i] * (double)xr[i];
+    for (int c = threadIdx.x * V; c < width; c += EW_THREADS * V) {
+        Cols<V> a;
+        a.load(xr + c);
+#pragma unroll
+        for (int k = 0; k < V; ++k) s += (double)a.v[k] * (double)a.v[k];
+    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
     __syncthreads();
-    const double tot = ((sh[0] + sh[1]) + sh[2]) + sh[3];
-    const float mean = (float)(tot / (double)width);
-    const float scale = 1.0f / sqrtf(mean + eps);
-    __syncthreads();  // x may alias out
-    for (int i = threadIdx.x; i < width; i += 256) {
-        float v = xr[i] * scale;
-        if (post != 1.0f) v = v * post;
-        if (w) v = v * w[i];
-        o[i] = v;
+    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float scale = 1.0f / sqrtf((float)(tot / (double)width) + eps);
+    for (int c = threadIdx.x * V; c < width; c += EW_THREADS * V) {
+        Cols<V> a;
+        a.load(xr + c);
+        Cols<V> g;
+        if (w) g.load(w + c);
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            float v = a.v[k] * scale;
+            if (post != 1.0f) v = v * post;
+            if (w) v = v * g.v[k];
+            a.v[k] = v;
+        }
+        a.store(o + c);
     }
 }
 
@@ -470,35 +517,65 @@ __global__ __launch_bounds__(64) void k_q4_mm_n(Q4Mats mats, const float *__rest
     q4_mm_rows<SUB, NCOL, QRW, TT>(mats.w[m], x, mats.y[m], mats.n_out[m], k, n_in, blockIdx.x - mats.start[m]);
 }
 
-__global__ void k_geglu_split(const float *__restrict__ gu, float *__restrict__ out, size_t n, int ff) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const size_t r = i / ff, j = i % ff;
-    out[i] = gelu(gu[r * 2 * ff + j]) * gu[r * 2 * ff + ff + j];
-}
-
-__global__ void k_gather_rows(const float *__restrict__ src, const int32_t *__restrict__ idx, float *__restrict__ dst,
-                              int width) {
-    const float *s = src + (size_t)idx[blockIdx.x] * width;
-    float *d = dst + (size_t)blockIdx.x * width;
-    for (int i = threadIdx.x; i < width; i += blockDim.x) d[i] = s[i];
-}
-
-// Slot order, (y * scale) * weight, first term assigned: bitwise the CPU combine
-// (runtime/src/exec.rs:626-638; runtime/tests/hip_ops.rs:421-439).
-__global__ void k_moe_combine(const float *__restrict__ y, const int32_t *__restrict__ pos,
-                              const float *__restrict__ scale, const float *__restrict__ weight,
-                              float *__restrict__ out, int used, int width) {
-    const int t = blockIdx.x;
-    for (int i = threadIdx.x; i < width; i += blockDim.x) {
-        float acc = 0.0f;
-        for (int j = 0; j < used; ++j) {
-            const int p = t * used + j;
-            const float v = y[(size_t)pos[p] * width + i] * scale[p] * weight[p];
-            acc = j == 0 ? v : acc + v;
-        }
-        out[(size_t)t * width + i] = acc;
+// Workgroup b takes row b / chunks, columns of chunk b % chunks (EW_THREADS V columns each).
+struct EwTile {
+    size_t row;
+    int col;
+    __device__ __forceinline__ EwTile(int chunks, int V) {
+        row = blockIdx.x / (unsigned)chunks;
+        col = ((int)(blockIdx.x % (unsigned)chunks) * EW_THREADS + (int)threadIdx.x) * V;
     }
+};
+
+// out[r][j] = gelu(gu[r][j]) * gu[r][ff + j]: the gate half, then the up half of each row of gu
+// (runtime/src/ops.rs:145-149; gelu is the reference's tanh form with the reference hosts' tanhf).
+template <int V>
+__global__ __launch_bounds__(EW_THREADS) void k_geglu_split(const float *__restrict__ gu, float *__restrict__ out,
+                                                            int ff, int chunks) {
+    const EwTile at(chunks, V);
+    if (at.col >= ff) return;
+    Cols<V> g, u;
+    g.load(gu + at.row * 2 * ff + at.col);
+    u.load(gu + at.row * 2 * ff + ff + at.col);
+#pragma unroll
+    for (int k = 0; k < V; ++k) g.v[k] = gelu(g.v[k]) * u.v[k];
+    g.store(out + at.row * ff + at.col);
+}
+
+// dst[r] = src[idx[r]], row by row.
+template <int V>
+__global__ __launch_bounds__(EW_THREADS) void k_gather_rows(const float *__restrict__ src, const int32_t *__restrict__ idx,
+                                                            float *__restrict__ dst, int width, int chunks) {
+    const EwTile at(chunks, V);
+    if (at.col >= width) return;
+    Cols<V> a;
+    a.load(src + (size_t)idx[at.row] * width + at.col);
+    a.store(dst + at.row * width + at.col);
+}
+
+// out[t] = sum over the token's slots j in order of (y[pos[p]] * scale[p]) * weight[p], p = t used + j,
+// the first term assigned (runtime/src/exec.rs:626-638; runtime/tests/hip_ops.rs:421-439 checks it
+// bit for bit). The slot's position, scale and weight are the same for the whole workgroup.
+template <int V>
+__global__ __launch_bounds__(EW_THREADS) void k_moe_combine(const float *__restrict__ y, const int32_t *__restrict__ pos,
+                                                            const float *__restrict__ scale,
+                                                            const float *__restrict__ weight, float *__restrict__ out,
+                                                            int used, int width, int chunks) {
+    const EwTile at(chunks, V);
+    if (at.col >= width) return;
+    Cols<V> acc;
+    for (int j = 0; j < used; ++j) {
+        const size_t p = at.row * used + j;
+        const float sc = scale[p], wt = weight[p];
+        Cols<V> a;
+        a.load(y + (size_t)pos[p] * width + at.col);
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            const float v = a.v[k] * sc * wt;
+            acc.v[k] = j == 0 ? v : acc.v[k] + v;
+        }
+    }
+    acc.store(out + at.row * width + at.col);
 }
 
 // a matrix of n_out rows of k goes through k_q4_mm_i8 (whatever the token count)
@@ -556,7 +633,10 @@ extern "C" {
 
 int rvh_rms_norm(const float *x, float *out, const float *weight, int rows, int width, float eps, float post) {
     RVM_CHECK(x && out && rows > 0 && width > 0);
-    hipLaunchKernelGGL(k_rms_norm, dim3(rows), dim3(256), 0, cur_stream(), x, out, weight, width, eps, post);
+    if (cols4(width, {x, out, weight}))
+        hipLaunchKernelGGL(k_rms_norm<4>, dim3(rows), dim3(EW_THREADS), 0, cur_stream(), x, out, weight, width, eps, post);
+    else
+        hipLaunchKernelGGL(k_rms_norm<1>, dim3(rows), dim3(EW_THREADS), 0, cur_stream(), x, out, weight, width, eps, post);
     return launched();
 }
 
@@ -633,24 +713,46 @@ int rvh_q4_mv(const void *w, const float *x, float *y, int n_out, int k, int n_i
     return rvh_q4_mm(w, x, y, n_out, k, n_in);
 }
 
+// The flat grid of the element-wise operators: rows x column chunks workgroups (at most 2^31 - 1).
+inline int ew_chunks(int width, int V) { return grid_blocks(width, EW_THREADS * V); }
+inline bool ew_grid_ok(int rows, int chunks) { return (long)rows * chunks <= 0x7fffffffL; }
+
 int rvh_geglu_split(const float *gu, float *out, int rows, int ff) {
     RVM_CHECK(gu && out && rows > 0 && ff > 0);
-    const size_t n = (size_t)rows * ff;
-    hipLaunchKernelGGL(k_geglu_split, dim3(grid_blocks(n, 256)), dim3(256), 0, cur_stream(), gu, out, n, ff);
+    const int V = cols4(ff, {gu, out}) ? 4 : 1, chunks = ew_chunks(ff, V);
+    RVM_CHECK(ew_grid_ok(rows, chunks));
+    const dim3 grid((unsigned)((long)rows * chunks));
+    if (V == 4)
+        hipLaunchKernelGGL(k_geglu_split<4>, grid, dim3(EW_THREADS), 0, cur_stream(), gu, out, ff, chunks);
+    else
+        hipLaunchKernelGGL(k_geglu_split<1>, grid, dim3(EW_THREADS), 0, cur_stream(), gu, out, ff, chunks);
     return launched();
 }
 
 int rvh_gather_rows(const float *src, const int32_t *idx, float *dst, int n, int width) {
     RVM_CHECK(src && idx && dst && n > 0 && width > 0);
-    hipLaunchKernelGGL(k_gather_rows, dim3(n), dim3(256), 0, cur_stream(), src, idx, dst, width);
+    const int V = cols4(width, {src, dst}) ? 4 : 1, chunks = ew_chunks(width, V);
+    RVM_CHECK(ew_grid_ok(n, chunks));
+    const dim3 grid((unsigned)((long)n * chunks));
+    if (V == 4)
+        hipLaunchKernelGGL(k_gather_rows<4>, grid, dim3(EW_THREADS), 0, cur_stream(), src, idx, dst, width, chunks);
+    else
+        hipLaunchKernelGGL(k_gather_rows<1>, grid, dim3(EW_THREADS), 0, cur_stream(), src, idx, dst, width, chunks);
     return launched();
 }
 
 int rvh_moe_combine(const float *y, const int32_t *pos, const float *scale, const float *weight, float *out,
                     int n_tok, int used, int width) {
     RVM_CHECK(y && pos && scale && weight && out && n_tok > 0 && used > 0 && width > 0);
-    hipLaunchKernelGGL(k_moe_combine, dim3(n_tok), dim3(256), 0, cur_stream(), y, pos, scale, weight, out, used,
-                       width);
+    const int V = cols4(width, {y, out}) ? 4 : 1, chunks = ew_chunks(width, V);
+    RVM_CHECK(ew_grid_ok(n_tok, chunks));
+    const dim3 grid((unsigned)((long)n_tok * chunks));
+    if (V == 4)
+        hipLaunchKernelGGL(k_moe_combine<4>, grid, dim3(EW_THREADS), 0, cur_stream(), y, pos, scale, weight, out, used,
+                           width, chunks);
+    else
+        hipLaunchKernelGGL(k_moe_combine<1>, grid, dim3(EW_THREADS), 0, cur_stream(), y, pos, scale, weight, out, used,
+                           width, chunks);
     return launched();
 }
 
