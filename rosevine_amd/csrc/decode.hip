@@ -108,8 +108,8 @@ __device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const
     uint32_t sv[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        wv[i] = nib[base + (size_t)i * 64];
-        sv[i] = scl[base + (size_t)i * 64];
+        wv[i] = ld_stream(nib + base + (size_t)i * 64);
+        sv[i] = ld_stream(scl + base + (size_t)i * 64);
     }
     // down entries of block t: RVM_PACK_ROWS32 with Sd = T / 2 steps; row r is lane
     // (r & 31) + 32 * (t / Sd) of tile r / 32 at step t % Sd
@@ -120,8 +120,8 @@ __device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const
     for (int i = 0; i < RD; ++i) {
         const int r = min((int)threadIdx.x + i * GU_WAVES * 64, d - 1);
         const size_t ent = (((size_t)e * Td + (r >> 5)) * Sd + sd) * 64 + 32 * half + (r & 31);
-        dv[i] = dnib[ent];
-        ds[i] = dscl[ent];
+        dv[i] = ld_stream(dnib + ent);
+        ds[i] = ld_stream(dscl + ent);
     }
     __builtin_amdgcn_sched_barrier(0);
     float tv[PER];

@@ -102,6 +102,15 @@ __device__ __forceinline__ float gelu(float x) {
     return 0.5f * x * (1.0f + tanhf_select(inner));
 }
 
+// Loads with the nontemporal hint, for expert weights that one call reads once: they then do not push
+// the router rows and the activations out of the caches.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream(const uint4 *p) {
+    const u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ld_stream(const uint16_t *p) { return __builtin_nontemporal_load(p); }
+
 // One block's term of the reference dot, (sumi as f32) * (d_w * d_x), each product rounded
 // (runtime/src/expert_kernel.rs:158); the reference folds these terms in block order from 0.0.
 __device__ __forceinline__ float block_term(int sumi, float dw, float dx) { return (float)sumi * (dw * dx); }
