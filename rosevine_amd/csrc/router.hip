@@ -458,7 +458,18 @@ __global__ __launch_bounds__(256) void k_select_exact(const float *__restrict__ 
 // contiguous chunk of pairs; per-(wave, expert) counts are scanned in (expert, wave) order, then
 // each wave places its pairs 64 at a time, ranking equal experts among lower lanes with ballots.
 // Ids outside [0, n_exp) are neither counted nor placed (pos_of = -1). With tiles (and tiles2)
-// set, every group is also cut into tiles of up to cap (cap2) pairs.
+// set, every group is also cut into tiles of up to cap (cap2) pairs. A wave reads its ids PLAN_R
+// rows of 64 at a time, the loads of a batch issued together; a chunk of at most PLAN_R rows (up to
+// 8192 pairs) stays in registers from the count to the placement.
+constexpr int PLAN_R = 8;
+__device__ __forceinline__ void plan_load(const int32_t *__restrict__ ids, int base, int hi, int lane,
+                                          int (&ev)[PLAN_R]) {
+#pragma unroll
+    for (int r = 0; r < PLAN_R; ++r) {
+        const int i = base + 64 * r + lane;
+        ev[r] = i < hi ? ids[i] : -1;
+    }
+}
 __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, int n, int n_exp,
                                                int32_t *__restrict__ order, int32_t *__restrict__ pos_of,
                                                int32_t *__restrict__ gstart, int32_t *__restrict__ tiles, int cap,
@@ -466,13 +477,18 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
     __shared__ int cnt[16][256];
     __shared__ int tot[257];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int i = threadIdx.x; i < 16 * 256; i += 1024) (&cnt[0][0])[i] = 0;
-    __syncthreads();
     const int chunk = ((n + 15) / 16 + 63) / 64 * 64;
     const int lo = w * chunk, hi = min(n, lo + chunk);
-    for (int i = lo + lane; i < hi; i += 64) {
-        const int e = ids[i];
-        if (e >= 0 && e < n_exp) atomicAdd(&cnt[w][e], 1);
+    const bool one_batch = chunk <= 64 * PLAN_R;
+    int ev[PLAN_R];
+    if (one_batch) plan_load(ids, lo, hi, lane, ev);  // in flight while the counts are cleared
+    for (int i = threadIdx.x; i < 16 * 256; i += 1024) (&cnt[0][0])[i] = 0;
+    __syncthreads();
+    for (int base = lo; base < hi; base += 64 * PLAN_R) {
+        if (!one_batch) plan_load(ids, base, hi, lane, ev);
+#pragma unroll
+        for (int r = 0; r < PLAN_R; ++r)
+            if (ev[r] >= 0 && ev[r] < n_exp) atomicAdd(&cnt[w][ev[r]], 1);
     }
     __syncthreads();
     if ((int)threadIdx.x < n_exp) {
@@ -542,25 +558,30 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
         }
     }
     __syncthreads();
-    for (int base = lo; base < hi; base += 64) {
-        const int i = base + lane;
-        const int raw = i < hi ? ids[i] : -1;
-        const bool valid = raw >= 0 && raw < n_exp;
-        const int e = valid ? raw : 0;
-        if (i < hi && !valid) pos_of[i] = -1;  // an id outside [0, n_exp) is left out of the plan
-        uint64_t m = __ballot(valid);
+    for (int base0 = lo; base0 < hi; base0 += 64 * PLAN_R) {
+        if (!one_batch) plan_load(ids, base0, hi, lane, ev);
 #pragma unroll
-        for (int bit = 0; bit < 8; ++bit) {
-            const bool set = (e >> bit) & 1;
-            const uint64_t b = __ballot(valid && set);
-            m &= set ? b : ~b;
-        }
-        if (valid) {
-            const uint64_t below = (1ull << lane) - 1ull;
-            const int pos = cnt[w][e] + __popcll(m & below);
-            order[pos] = i;
-            pos_of[i] = pos;
-            if ((m >> lane) == 1ull) cnt[w][e] = pos + 1;  // highest lane of its group
+        for (int r = 0; r < PLAN_R; ++r) {
+            const int base = base0 + 64 * r;
+            if (base >= hi) break;  // wave-uniform
+            const int i = base + lane, raw = ev[r];
+            const bool valid = raw >= 0 && raw < n_exp;
+            const int e = valid ? raw : 0;
+            if (i < hi && !valid) pos_of[i] = -1;  // an id outside [0, n_exp) is left out of the plan
+            uint64_t m = __ballot(valid);
+#pragma unroll
+            for (int bit = 0; bit < 8; ++bit) {
+                const bool set = (e >> bit) & 1;
+                const uint64_t b = __ballot(valid && set);
+                m &= set ? b : ~b;
+            }
+            if (valid) {
+                const uint64_t below = (1ull << lane) - 1ull;
+                const int pos = cnt[w][e] + __popcll(m & below);
+                order[pos] = i;
+                pos_of[i] = pos;
+                if ((m >> lane) == 1ull) cnt[w][e] = pos + 1;  // highest lane of its group
+            }
         }
     }
 }

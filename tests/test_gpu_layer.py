@@ -101,7 +101,9 @@ def test_router_fold_path_is_the_references_bits(gpu, orc, n, bias, pre):
 
 def test_plan_matches_oracle(gpu, orc):
     rng = np.random.default_rng(6)
-    for n_pairs in [8, 256, 3000, 4096]:
+    # up to 8192 pairs a wave keeps its ids in registers between the count and the placement; above
+    # that it reads them in batches (9001 and 40000: partial and several batches per wave)
+    for n_pairs in [8, 256, 3000, 4096, 8192, 9001, 40000]:
         ids = (rng.zipf(1.2, n_pairs) % N_EXP).astype(np.int32)
         order, pos_of, gs = DevBuf(n_pairs * 4), DevBuf(n_pairs * 4), DevBuf((N_EXP + 1) * 4)
         hip.moe_plan(dev(ids), n_pairs, N_EXP, order, pos_of, gs)
@@ -109,6 +111,17 @@ def test_plan_matches_oracle(gpu, orc):
         assert np.array_equal(order.download(np.int32, n_pairs), o.astype(np.int32))
         assert np.array_equal(pos_of.download(np.int32, n_pairs), p.astype(np.int32))
         assert np.array_equal(gs.download(np.int32, N_EXP + 1), g.astype(np.int32))
+        if n_pairs > 4096:  # a few ids out of range among them: a stable sort of the others
+            ids[rng.integers(0, n_pairs, 7)] = -1
+            hip.moe_plan(dev(ids), n_pairs, N_EXP, order, pos_of, gs)
+            keep = np.flatnonzero(ids >= 0)
+            o = keep[np.argsort(ids[keep], kind="stable")]
+            p = np.full(n_pairs, -1, np.int64)
+            p[o] = np.arange(o.size)
+            g = np.concatenate([[0], np.cumsum(np.bincount(ids[keep], minlength=N_EXP))])
+            assert np.array_equal(order.download(np.int32, o.size), o.astype(np.int32))
+            assert np.array_equal(pos_of.download(np.int32, n_pairs), p.astype(np.int32))
+            assert np.array_equal(gs.download(np.int32, N_EXP + 1), g.astype(np.int32))
     # ids outside [0, n_exp) are left out of the plan
     ids = np.array([3, -1, 3, 200, 0], np.int32)
     order, pos_of, gs = DevBuf(20), DevBuf(20), DevBuf((N_EXP + 1) * 4)
