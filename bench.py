@@ -278,7 +278,7 @@ def measure_ragged_stack30(seed: int, n_layers: int = 30, n_tok: int = 32, steps
 
 def measure_batch(seed: int, n: int, routing: str, steps: int, stack: bool = False) -> dict:
     """One layer's forward over n tokens (rvm_moe_forward) on the current (non-default) stream: a graph
-    of 4 calls on 4 resident batches, replayed steps / 4 times after one warm-up replay and timed with
+    of 4 calls on 4 resident batches, replayed steps / 4 times after three warm-up replays and timed with
     HIP events on that stream. routing:
     "iid" (no bias), "skewed" (the 30-layer configuration's per-expert bias N(0,1): groups of 0 to a few
     hundred pairs, some experts empty) or "zipf" (Zipf(1.1) popularity). Reports the time, the HBM and
@@ -299,13 +299,14 @@ def measure_batch(seed: int, n: int, routing: str, steps: int, stack: bool = Fal
         moe.forward(layer, xs[it[0] % 4], out, n, ws)
         it[0] += 1
 
-    # graph-launched like the decode line: one graph of the 4 batches, replayed
+    # graph-launched like the decode line: one graph of the 4 batches, replayed; three warm-up replays
+    # (the first passes over freshly allocated weights also pay their page-table walks)
     hip.Graph.begin()
     for _ in range(4):
         run()
     g = hip.Graph.end()
     reps = max(1, steps // 4)
-    ms = _timed(g.launch, reps, 1) / 4
+    ms = _timed(g.launch, reps, 3) / 4
     g.close()
     moe.forward(layer, xs[0], out, n, ws)
     ids, _ = ws.selection(layer, n)
@@ -759,8 +760,8 @@ def main() -> int:
         st3 = hip.Stream()
         st3.use()
         batches = {}
-        for name, n, routing, steps in [("prefill512", 512, "iid", 20), ("prefill512_skewed", 512, "skewed", 20),
-                                        ("ragged32", 32, "zipf", 100)]:
+        for name, n, routing, steps in [("prefill512", 512, "iid", 100), ("prefill512_skewed", 512, "skewed", 100),
+                                        ("ragged32", 32, "zipf", 400)]:
             log(f"[bench] {name}")
             batches[name] = measure_batch(args.seed, n, routing, steps, stack=n == 32 and not args.no_stack)
             log(f"[bench] {name}: {batches[name]['us']} us")
