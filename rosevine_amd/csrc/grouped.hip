@@ -9,7 +9,7 @@
 //   k_gateup_quad,        -> 4-pair tiles: one wave per (tile, 64 weight rows); the 16-block
 //   k_down_quad              v_mfma_i32_4x4x4_16b_i8 gives each lane its row's exact block sums
 //                            for the 4 pairs, so the f32 fold spends nothing on empty pair places
-//   k_gateup_mfma         -> per (tile, 4 row tiles of 32 gate + 32 up rows): int8 MFMA
+//   k_gateup_mfma         -> per (tile, 2 row tiles of 32 gate + 32 up rows, half a tile a wave): int8 MFMA
 //                            (v_mfma_i32_16x16x32_i8, one 32-weight block per instruction) gives
 //                            each block's exact int32 sum for 16 pairs x 16 rows; the f32 terms
 //                            (sumi as f32) * (d_w * d_x) are folded in block order per output, as
@@ -77,30 +77,31 @@ __device__ __forceinline__ void fold_block(float (&acc)[4], v4i sumi, float dw, 
     acc[3] = acc[3] + (float)sumi[3] * (dw * dx.w);
 }
 
-template <int MT, int NR, int KC>
+template <int MT, int NR, int KC, int W = MW>
 struct TileLds {
     static constexpr int R = 16 * MT, XP = KC * QK + 16;  // row pitch: conflict-free 8-byte reads
     alignas(16) int8_t xs[2][R * XP];           // activation rows of the chunk
     alignas(16) float ss[2][KC * R];            // their block scales, [block][row]
-    alignas(16) uint16_t ws[MW][KC * 16 * NR];  // per wave: weight scales, [block][m][piece]
+    alignas(16) uint16_t ws[W][KC * 16 * NR];   // per wave: weight scales, [block][m][piece]
     int row_of[R];                              // source row of each tile place, -1 when empty
 };
 
 // The block sums of one tile: rows of the wave's row tile (entry groups tb .. tb+S-1, NR pieces of
-// 16 plane lanes; block b uses group b mod S at lane offset 32 (b / S)) against the tile's R
+// 16 plane lanes, pieces p0, p0 + PS, ..., wave-uniform; block b uses group b mod S at lane offset
+// 32 (b / S)) against the tile's R
 // activation rows (K = width, nb = width / 32 blocks). acc[mt][r][i] is the output of pair
 // 16 mt + 4 g + i and plane lane 16 r + m, for lane = 16 g + m. Only the first LIVE m-tiles are
 // computed (the others hold no pair; their acc stays 0). All waves take part in the staging and
 // barriers; waves without a row tile (active false) skip the weights and MFMAs.
-template <int MT, int NR, int KC, int LIVE>
+template <int MT, int NR, int KC, int LIVE, int W = MW, int PS = 1>
 __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const uint16_t *__restrict__ scl,
                                           size_t tb, int S, bool active, const int8_t *__restrict__ src,
-                                          const float *__restrict__ ssrc, int width, TileLds<MT, NR, KC> &sh,
-                                          float (&acc)[MT][NR][4]) {
+                                          const float *__restrict__ ssrc, int width, TileLds<MT, NR, KC, W> &sh,
+                                          float (&acc)[MT][NR][4], int p0 = 0) {
     // Every global load below is issued unconditionally (addresses clamped into the buffers, the
     // values selected when stored), so that the compiler can count the loads in flight and wait
     // for exactly the ones it needs: the next chunk's loads stay outstanding while this one runs.
-    constexpr int R = 16 * MT, NT = MW * 64, XP = TileLds<MT, NR, KC>::XP;
+    constexpr int R = 16 * MT, NT = W * 64, XP = TileLds<MT, NR, KC, W>::XP;
     constexpr int XU = KC * QK / 16;  // 16-byte pieces of a staged row chunk
     constexpr int XI = (R * XU + NT - 1) / NT, SI = (R * KC + NT - 1) / NT;
     constexpr int SPL = KC * 16 * NR / 64;  // weight scales per lane per chunk (2, 4 or 8)
@@ -152,14 +153,16 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
     }
 
     const int loff = m * 16 + 4 * g;  // this lane's byte in a piece of 16 plane entries
-    auto load_w = [&](int c, uint32_t (&wn)[KC][NR], uint32_t (&wsc)[SPL / 2]) {
+    constexpr int SW = SPL / 2;  // dwords of weight scales per lane per chunk
+    auto load_w = [&](int c, uint32_t (&wn)[KC][NR], uint32_t (&wsc)[SW]) {
 #pragma unroll
         for (int kb = 0; kb < KC; ++kb) {
             const uint8_t *pb = nib + entry(c * KC + kb) * 16;  // wave-uniform: a scalar base
 #pragma unroll
-            for (int r = 0; r < NR; ++r) wn[kb][r] = *(const uint32_t *)(pb + (256 * r + loff));
+            for (int r = 0; r < NR; ++r) wn[kb][r] = *(const uint32_t *)(pb + (256 * (p0 + PS * r) + loff));
         }
-        const uint16_t *sp = scl + entry(c * KC + skb) + sj;
+        // entries j, j+1, ... of the wave's pieces: plane lane 16 (p0 + PS (j / 16)) + j mod 16
+        const uint16_t *sp = scl + entry(c * KC + skb) + 16 * p0 + (sj & 15) + 16 * PS * (sj >> 4);
         if constexpr (SPL == 8) {
             const uint4 v = *(const uint4 *)sp;
             wsc[0] = v.x;
@@ -193,7 +196,7 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
             if (skbx[k] >= 0) sh.ss[buf][threadIdx.x + k * NT] = ok ? sr[k] * 0.0625f : 0.0f;  // d_x / 16
         }
     };
-    auto compute = [&](int c, int buf, const uint32_t (&wn)[KC][NR], const uint32_t (&wsc)[SPL / 2]) {
+    auto compute = [&](int c, int buf, const uint32_t (&wn)[KC][NR], const uint32_t (&wsc)[SW]) {
         if (!active) return;
         // the chunk's weight scales to [block][m][piece] in this wave's LDS
         uint16_t *wsw = sh.ws[w];
@@ -245,7 +248,7 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
     };
 
     uint32_t wn0[KC][NR], wn1[KC][NR];
-    uint32_t ws0[SPL / 2], ws1[SPL / 2];
+    uint32_t ws0[SW], ws1[SW];
     uint4 xr[XI];
     float sr[SI];
     load_x(0, xr, sr);
@@ -275,22 +278,27 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
     }
 }
 
-// Gate/up for one tile (blockIdx.y) of up to 16 MT pairs of expert e: wave w takes row tile
-// rt = 4 blockIdx.x + w
-// (32 gate rows and the matching 32 up rows, one RVM_PACK_GATE_UP tile; pieces 0, 1 are gate rows
-// m and 16 + m, pieces 2, 3 the up rows). h = gelu(gate) * up is quantised per pair to one Q8_0
-// block of 32 (runtime/src/ops.rs:95-105) and stored in the K order of kperm.
-template <int MT>
-__global__ __launch_bounds__(MW * 64) void k_gateup_mfma(const uint8_t *__restrict__ nib,
-                                                         const uint16_t *__restrict__ scl,
-                                                         const int32_t *__restrict__ tiles,
-                                                         const int32_t *__restrict__ gstart,
-                                                         const int32_t *__restrict__ order,
-                                                         const int8_t *__restrict__ xq8,
-                                                         const float *__restrict__ xsc, int8_t *__restrict__ hq8,
-                                                         float *__restrict__ hsc, int d, int ff, int top_k) {
+// Gate/up for one tile (blockIdx.y) of up to 16 MT pairs of expert e, TW row tiles per workgroup
+// (32 gate rows and the matching 32 up rows each, one RVM_PACK_GATE_UP tile), half a row tile per
+// wave: wave w takes row tile rt = TW blockIdx.x + w / 2, gate rows 16 h + m (piece h = w mod 2) and
+// the matching up rows (piece h + 2). Half-tile waves are twice as many, each half as long, at 112
+// VGPRs (four waves per SIMD, against three for whole row tiles at 168): the grid's last partial
+// round of workgroups leaves fewer SIMDs short of waves (512 tokens: 297 -> 275 us per call).
+// h = gelu(gate) * up is quantised per pair to one Q8_0 block of 32 (runtime/src/ops.rs:95-105) and
+// stored in the K order of kperm; the block spans both waves' rows, so they exchange their maxima of
+// |h| in LDS (a maximum of non-negative values, the same bits in any order).
+template <int MT, int TW>
+__global__ __launch_bounds__(128 * TW) void k_gateup_mfma(const uint8_t *__restrict__ nib,
+                                                          const uint16_t *__restrict__ scl,
+                                                          const int32_t *__restrict__ tiles,
+                                                          const int32_t *__restrict__ gstart,
+                                                          const int32_t *__restrict__ order,
+                                                          const int8_t *__restrict__ xq8,
+                                                          const float *__restrict__ xsc, int8_t *__restrict__ hq8,
+                                                          float *__restrict__ hsc, int d, int ff, int top_k) {
     constexpr int R = 16 * MT, KC = chunk_blocks<MT>();
-    __shared__ TileLds<MT, 4, KC> sh;
+    __shared__ TileLds<MT, 2, KC, 2 * TW> sh;
+    __shared__ float hmax[2 * TW][MT][4][4];  // [wave][m-tile][i][g]: max of |h| over the wave's 16 rows
     const int tile = blockIdx.y;
     if (tile >= tiles[0]) return;
     const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
@@ -298,33 +306,40 @@ __global__ __launch_bounds__(MW * 64) void k_gateup_mfma(const uint8_t *__restri
     const int nb = d / QK, Tg = ff / 32;
     if (threadIdx.x < R) sh.row_of[threadIdx.x] = (int)threadIdx.x < cnt ? order[k0 + threadIdx.x] / top_k : -1;
     __syncthreads();
-    // wave-uniform, so that the weight addresses are a scalar base and a lane offset
-    const int rt = blockIdx.x * MW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = wv & 1;
+    const int rt = blockIdx.x * TW + (wv >> 1);
     const bool active = rt < Tg;
-    float acc[MT][4][4];
-    // every m-tile, also an empty one: a second instance of the loop for tiles of at most 16 pairs
-    // measured slower here (the down kernel keeps one)
-    tile_sums<MT, 4, KC, MT>(nib, scl, ((size_t)e * Tg + (active ? rt : 0)) * nb, nb, active, xq8, xsc, d, sh, acc);
-    if (!active) return;
+    float acc[MT][2][4];
+    tile_sums<MT, 2, KC, MT, 2 * TW, 2>(nib, scl, ((size_t)e * Tg + (active ? rt : 0)) * nb, nb, active, xq8, xsc, d,
+                                        sh, acc, h);
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
+    float hv[MT][4];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
         if (mt * 16 >= cnt) break;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float h0 = gelu(acc[mt][0][i]) * acc[mt][2][i];
-            const float h1 = gelu(acc[mt][1][i]) * acc[mt][3][i];
-            const float amax = row16_max(fmaxf(fmaxf(0.0f, fabsf(h0)), fabsf(h1)));
+            hv[mt][i] = gelu(acc[mt][0][i]) * acc[mt][1][i];
+            const float mx = row16_max(fmaxf(0.0f, fabsf(hv[mt][i])));
+            if (m == 0) hmax[wv][mt][i][g] = mx;
+        }
+    }
+    __syncthreads();
+    if (!active) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        if (mt * 16 >= cnt) break;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float amax = fmaxf(hmax[wv & ~1][mt][i][g], hmax[wv | 1][mt][i][g]);
             const float dq = amax / 127.0f;
             const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
-            const uint16_t dbits = f2h_rne(dq);
-            const int q0 = sat_i8(roundf(h0 * id)), q1 = sat_i8(roundf(h1 * id));
+            const int q = sat_i8(roundf(hv[mt][i] * id));
             const int pr = mt * 16 + 4 * g + i;
             if (pr < cnt) {
                 int8_t *hrow = hq8 + (size_t)(k0 + pr) * ff + rt * QK;
-                hrow[kperm(m)] = (int8_t)q0;
-                hrow[kperm(16 + m)] = (int8_t)q1;
-                if (m == 0) hsc[(size_t)(k0 + pr) * Tg + rt] = h2f(dbits);
+                hrow[kperm(16 * h + m)] = (int8_t)q;
+                if (h == 0 && m == 0) hsc[(size_t)(k0 + pr) * Tg + rt] = h2f(f2h_rne(dq));
             }
         }
     }
@@ -352,7 +367,8 @@ __global__ __launch_bounds__(MW * 64) void k_down_mfma(const uint8_t *__restrict
     const int rt = blockIdx.x * MW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const bool active = rt < Td;
     float acc[MT][2][4];
-    // a tile runs the loop of its occupied m-tiles only
+    // a tile runs the loop of its occupied m-tiles only (half row tiles per wave, as in the gate/up
+    // kernel, measured slower here: 282 against 276.5 us for 512 tokens)
     const size_t tb = ((size_t)e * Td + (active ? rt : 0)) * Sd;
     if (MT > 1 && cnt <= 16)
         tile_sums<MT, 2, KC, 1>(nib, scl, tb, Sd, active, hq8, hsc, ff, sh, acc);
@@ -647,9 +663,9 @@ inline int tile_pairs(const rvm_layer *L, int n_tok) {
 }
 
 // The 16x16 MFMA kernels: gate/up on tiles of 16 MT pairs (lay.tiles), down on tiles of 16 MD pairs
-// (lay.tiles2). Gate/up keeps two m-tiles: with three its registers allow two waves per SIMD instead
-// of three (200 against 186 us for 512 tokens); down runs three at three waves per SIMD (73 against
-// 82.5 us), each of its tiles through the loop of only its occupied m-tiles.
+// (lay.tiles2). Gate/up keeps two m-tiles (with half row tiles per wave, three measured the same:
+// 276.5-277.9 against 277.8-278.9 us for 512 tokens); down runs three at three waves per SIMD (73
+// against 82.5 us), each of its tiles through the loop of only its occupied m-tiles.
 template <int MT, int MD>
 int launch_experts(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &lay) {
     const int32_t *tiles = (const int32_t *)(w + lay.tiles);
@@ -659,8 +675,10 @@ int launch_experts(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &la
     const size_t gu_entries = (size_t)L->n_exp * 2 * L->ff * (L->d / QK);
     const uint8_t *gnib = (const uint8_t *)L->gate_up;
     const uint16_t *gscl = (const uint16_t *)(gnib + gu_entries * 16);
-    hipLaunchKernelGGL(k_gateup_mfma<MT>, dim3(grid_blocks(L->ff / 32, MW), nt), dim3(MW * 64), 0, cur_stream(), gnib,
-                       gscl, tiles, gstart, (const int32_t *)(w + lay.order), (const int8_t *)(w + lay.xq8),
+    constexpr int TW = 2;  // row tiles per gate/up workgroup (one: 280 against 275 us for 512 tokens)
+    auto *gkern = k_gateup_mfma<MT, TW>;
+    hipLaunchKernelGGL(gkern, dim3(grid_blocks(L->ff / 32, TW), nt), dim3(128 * TW), 0, cur_stream(), gnib, gscl, tiles,
+                       gstart, (const int32_t *)(w + lay.order), (const int8_t *)(w + lay.xq8),
                        (const float *)(w + lay.xsc), (int8_t *)(w + lay.hq8), (float *)(w + lay.hsc), L->d, L->ff,
                        L->top_k);
     int rc = launched();
