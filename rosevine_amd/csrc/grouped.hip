@@ -283,7 +283,9 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
 // wave: wave w takes row tile rt = TW blockIdx.x + w / 2, gate rows 16 h + m (piece h = w mod 2) and
 // the matching up rows (piece h + 2). Half-tile waves are twice as many, each half as long, at 112
 // VGPRs (four waves per SIMD, against three for whole row tiles at 168): the grid's last partial
-// round of workgroups leaves fewer SIMDs short of waves (512 tokens: 297 -> 275 us per call).
+// round of workgroups leaves fewer SIMDs short of waves (512 tokens: 297 -> 275 us per call). A tile
+// of at most 16 pairs (the remainder of an expert's pairs after a full tile) runs the loop of its
+// one occupied m-tile (gate/up 144.9 -> 140.2 us; at 110 VGPRs the second instance costs no wave).
 // h = gelu(gate) * up is quantised per pair to one Q8_0 block of 32 (runtime/src/ops.rs:95-105) and
 // stored in the K order of kperm; the block spans both waves' rows, so they exchange their maxima of
 // |h| in LDS (a maximum of non-negative values, the same bits in any order).
@@ -310,8 +312,11 @@ __global__ __launch_bounds__(128 * TW) void k_gateup_mfma(const uint8_t *__restr
     const int rt = blockIdx.x * TW + (wv >> 1);
     const bool active = rt < Tg;
     float acc[MT][2][4];
-    tile_sums<MT, 2, KC, MT, 2 * TW, 2>(nib, scl, ((size_t)e * Tg + (active ? rt : 0)) * nb, nb, active, xq8, xsc, d,
-                                        sh, acc, h);
+    const size_t tb = ((size_t)e * Tg + (active ? rt : 0)) * nb;
+    if (MT > 1 && cnt <= 16)  // a tile of at most 16 pairs runs the loop of its one occupied m-tile
+        tile_sums<MT, 2, KC, 1, 2 * TW, 2>(nib, scl, tb, nb, active, xq8, xsc, d, sh, acc, h);
+    else
+        tile_sums<MT, 2, KC, MT, 2 * TW, 2>(nib, scl, tb, nb, active, xq8, xsc, d, sh, acc, h);
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
     float hv[MT][4];
 #pragma unroll
