@@ -330,10 +330,37 @@ __device__ __forceinline__ void fold_quads(float &acc, const float4 &w, const fl
     (fold_quad2<BASE + 2 * Q, BASE + 2 * Q + 1>(acc, w, xv[2 * Q], xv[2 * Q + 1]), ...);
 }
 
+// The Q8_0 blocks of 32 router-input values of one token, all in this thread (v[4 i + k] = quad i's
+// element k), stored as k_router_prep stores them: the same numbers as quant_q8_half's, whose block
+// maximum (of non-negative values, NaN ignored) is the same in any order; quant j at byte kperm(j),
+// so quad i (elements 4i .. 4i+3) is dword 2 (i mod 4) + i / 4.
+__device__ __forceinline__ void quant_q8_block(const float4 (&v)[8], int8_t *__restrict__ dst, float *__restrict__ dsc) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        m = fmaxf(m, fmaxf(fmaxf(fmaxf(0.0f, fabsf(v[i].x)), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    const float dq = m / 127.0f;
+    const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
+    uint32_t dw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t b0 = (uint8_t)sat_i8(roundf(v[i].x * id)), b1 = (uint8_t)sat_i8(roundf(v[i].y * id));
+        const uint32_t b2 = (uint8_t)sat_i8(roundf(v[i].z * id)), b3 = (uint8_t)sat_i8(roundf(v[i].w * id));
+        dw[2 * (i & 3) + (i >> 2)] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+    }
+    ((uint4 *)dst)[0] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+    ((uint4 *)dst)[1] = make_uint4(dw[4], dw[5], dw[6], dw[7]);
+    *dsc = h2f(f2h_rne(dq));
+}
+
+// With xq8 set (batches whose router input is x itself), the workgroups also write the tokens'
+// Q8_0 blocks for the expert kernels, which k_router_prep writes otherwise: expert group g of a
+// token tile quantises the chunks c = g, g + groups, ... of the tile's staged input, one block of
+// one token per thread.
 template <int F4>
 __global__ __launch_bounds__(FW * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_router_fold(
     const float *__restrict__ W, const float *__restrict__ xin, const float *__restrict__ bias, int n_tok, int n_exp,
-    float *__restrict__ R) {
+    float *__restrict__ R, int8_t *__restrict__ xq8, float *__restrict__ xsc) {
     constexpr int d = 256 * F4, NCH = d / FKC, KQ = FKC / 4, LD = 64 * KQ / (FW * 64), SQ = 8, RS = KQ / SQ;
     constexpr int WQ = d / 4, WL = (FW * WQ + FW * 64 - 1) / (FW * 64);  // row quads, and per thread
     static_assert(FKC == 128 && NCH % 2 == 0 && RS == 4, "two 64-column row blocks and four sub-steps per chunk");
@@ -393,8 +420,20 @@ __global__ __launch_bounds__(FW * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
     // buffer was last read in chunk c - 1), then p loads chunk c + 3. Sub-step r folds quads
     // 8r .. 8r+7 while the tokens' quads of sub-step r + 1 come from LDS; the scheduling barriers
     // keep each sub-step's reads in their place.
+    const int groups = (n_exp + FW - 1) / FW, g = (int)(blockIdx.x / tiles);
     auto chunk = [&](int c, float4 (&p)[LD]) {
         const int buf = c & 1;
+        if (xq8 && c % groups == g) {  // block tid / 64 of chunk c for token tid % 64
+            const int tt = tid & 63, kb = tid >> 6;
+            static_assert(FW * 64 == 64 * (FKC / QK), "one block of one token per thread");
+            if (t0 + tt < n_tok) {
+                float4 v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = xs[buf][8 * kb + i][tt ^ i];
+                const int hb = c * (FKC / QK) + kb;
+                quant_q8_block(v, xq8 + (size_t)(t0 + tt) * d + hb * QK, xsc + (size_t)(t0 + tt) * (d / QK) + hb);
+            }
+        }
         float4 wb[2];
 #pragma unroll
         for (int k = 0; k < 2; ++k) wb[k] = wrow[(2 * c + k) * 16];
@@ -600,12 +639,18 @@ int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, cons
             // R (the logits) in the statistics region; the normed router input in the region of the
             // down rows y (pairs x d floats, at least n_tok x d), which the expert kernels write later
             float *R = (float *)(ws + lay.stats), *rin = (float *)(ws + lay.y);
-            hipLaunchKernelGGL(k_router_prep<F4>, dim3(n_tok), dim3(256), 0, cur_stream(), x, n_tok, xf, rin,
-                               (int8_t *)(ws + lay.xq8), (float *)(ws + lay.xsc));
-            if (int rc = launched()) return rc;
+            // with the norm, k_router_prep forms the router and expert inputs and the Q8_0 blocks;
+            // without it the router input is x, and the fold's workgroups write the Q8_0 blocks
+            int8_t *xq8 = (int8_t *)(ws + lay.xq8);
+            float *xsc = (float *)(ws + lay.xsc);
+            if (pre) {
+                hipLaunchKernelGGL(k_router_prep<F4>, dim3(n_tok), dim3(256), 0, cur_stream(), x, n_tok, xf, rin, xq8,
+                                   xsc);
+                if (int rc = launched()) return rc;
+            }
             hipLaunchKernelGGL(k_router_fold<F4>, dim3(grid_blocks(L->n_exp, FW) * grid_blocks(n_tok, 64)),
                                dim3(FW * 64), 0, cur_stream(), L->router, pre ? rin : x, L->router_bias, n_tok,
-                               L->n_exp, R);
+                               L->n_exp, R, pre ? nullptr : xq8, pre ? nullptr : xsc);
             if (int rc = launched()) return rc;
             hipLaunchKernelGGL(k_select_exact, dim3(grid_blocks(n_tok, 4)), dim3(256), 0, cur_stream(), R, n_tok,
                                L->n_exp, L->top_k, ids, wts, logits);
