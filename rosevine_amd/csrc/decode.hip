@@ -90,7 +90,7 @@ union GateUpShared {
 //   (sumi as f32) * (d_w * d_h) of rows i, i + 512, ... (their entries are loaded with the gate/up
 //   ones) and writes them to dterm[r]; the down kernel folds each row's T terms in block order.
 // Called by every thread.
-template <int PER, bool STAGE, class St>
+template <int PER, bool STAGE, bool NT, class St>
 __device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl,
                                             const uint4 *__restrict__ dnib, const uint16_t *__restrict__ dscl,
                                             int e, int t, int T, const St &st, uint4 *act, float (*terms)[64],
@@ -108,8 +108,8 @@ __device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const
     uint32_t sv[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        wv[i] = ld_stream(nib + base + (size_t)i * 64);
-        sv[i] = ld_stream(scl + base + (size_t)i * 64);
+        wv[i] = ld_weights<NT>(nib + base + (size_t)i * 64);
+        sv[i] = ld_weights<NT>(scl + base + (size_t)i * 64);
     }
     // down entries of block t: RVM_PACK_ROWS32 with Sd = T / 2 steps; row r is lane
     // (r & 31) + 32 * (t / Sd) of tile r / 32 at step t % Sd
@@ -120,8 +120,8 @@ __device__ __forceinline__ void gateup_tile(const uint4 *__restrict__ nib, const
     for (int i = 0; i < RD; ++i) {
         const int r = min((int)threadIdx.x + i * GU_WAVES * 64, d - 1);
         const size_t ent = (((size_t)e * Td + (r >> 5)) * Sd + sd) * 64 + 32 * half + (r & 31);
-        dv[i] = ld_stream(dnib + ent);
-        ds[i] = ld_stream(dscl + ent);
+        dv[i] = ld_weights<NT>(dnib + ent);
+        ds[i] = ld_weights<NT>(dscl + ent);
     }
     __builtin_amdgcn_sched_barrier(0);
     float tv[PER];
@@ -168,7 +168,7 @@ __device__ __forceinline__ int clamp_expert(int e, int n_exp) { return (unsigned
 // (hslot): the slot of the S ranking that computed the same expert, or a correction row that it
 // computes itself for an expert the S ranking missed. Workgroups 1.. each take slot (b / T),
 // tile (b % T) of the S ranking's experts.
-template <int PER>  // steps per wave = (d / 32) / GU_WAVES = d / 256
+template <int PER, bool NT>  // steps per wave = (d / 32) / GU_WAVES = d / 256; NT: streaming weight loads
 __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
     const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl, const uint4 *__restrict__ dnib,
     const uint16_t *__restrict__ dscl, const double2 *__restrict__ stats, const float *__restrict__ bias,
@@ -197,7 +197,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
                                            ctl, nullptr);
         const int e = __builtin_amdgcn_readfirstlane(clamp_expert(spec_id(u.sel, slot, top_k), n_exp));
         RVM_STAMP(g_stamp, 0, 1);
-        gateup_tile<PER, true>(nib, scl, dnib, dscl, e, t, T, st, act, u.terms, (uint32_t *)hprep,
+        gateup_tile<PER, true, NT>(nib, scl, dnib, dscl, e, t, T, st, act, u.terms, (uint32_t *)hprep,
                                hact + ((size_t)slot * T + t) * ACT_DW, dterm + ((size_t)slot * T + t) * d);
         return;
     }
@@ -230,10 +230,10 @@ __global__ __launch_bounds__(GU_WAVES * 64) void k_gateup_decode(
         for (int t = 0; t < T; ++t) {
             const size_t row = (size_t)(top_k + m) * T + t;
             if (m == 0 && t == 0)
-                gateup_tile<PER, true>(nib, scl, dnib, dscl, fix_e[m], t, T, st, act, u.terms, (uint32_t *)hprep,
+                gateup_tile<PER, true, NT>(nib, scl, dnib, dscl, fix_e[m], t, T, st, act, u.terms, (uint32_t *)hprep,
                                        hact + row * ACT_DW, dterm + row * d);
             else
-                gateup_tile<PER, false>(nib, scl, dnib, dscl, fix_e[m], t, T, st, act, u.terms, (uint32_t *)hprep,
+                gateup_tile<PER, false, NT>(nib, scl, dnib, dscl, fix_e[m], t, T, st, act, u.terms, (uint32_t *)hprep,
                                         hact + row * ACT_DW, dterm + row * d);
         }
 }
@@ -296,7 +296,7 @@ namespace rvm {
 
 // One decode token through the layer, scratch in ws (ws_layout(L, 1) bytes).
 int moe_decode(const rvm_layer *L, const float *x, float *out, int flags, const XForm &xf, void *ws,
-               size_t ws_bytes) {
+               size_t ws_bytes, bool stream) {
     RVM_CHECK(layer_ok(L) && x && out && ws);
     const WsLayout lay = ws_layout(L, 1);
     RVM_CHECK(ws_bytes >= lay.total);
@@ -315,10 +315,12 @@ int moe_decode(const rvm_layer *L, const float *x, float *out, int flags, const 
     const uint16_t *dscl = (const uint16_t *)((const uint8_t *)L->down + dn_entries * 16);
     const int exact = (flags & RVM_EXACT_SELECT) ? 1 : 0;
     rc = with_steps(L->d / 256, [&](auto per) {
-        hipLaunchKernelGGL(k_gateup_decode<decltype(per)::value>, dim3(1 + L->top_k * Tg), dim3(GU_WAVES * 64), 0,
-                           cur_stream(), gnib, gscl, dnib, dscl, (const double2 *)(w + lay.stats), L->router_bias,
-                           L->router, x, L->n_exp, L->top_k, xf, exact, (uint32_t *)(w + lay.ctl), ids, wts,
-                           (const uint4 *)(w + lay.xact), (uint32_t *)(w + lay.hact), (float *)(w + lay.dterm), Tg);
+        constexpr int PER = decltype(per)::value;
+        auto *kern = stream ? k_gateup_decode<PER, true> : k_gateup_decode<PER, false>;
+        hipLaunchKernelGGL(kern, dim3(1 + L->top_k * Tg), dim3(GU_WAVES * 64), 0, cur_stream(), gnib, gscl, dnib, dscl,
+                           (const double2 *)(w + lay.stats), L->router_bias, L->router, x, L->n_exp, L->top_k, xf,
+                           exact, (uint32_t *)(w + lay.ctl), ids, wts, (const uint4 *)(w + lay.xact),
+                           (uint32_t *)(w + lay.hact), (float *)(w + lay.dterm), Tg);
         return launched();
     });
     if (rc) return rc;

@@ -699,9 +699,9 @@ int launch_experts(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &la
 }
 
 int moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int flags, const XForm &xf, void *ws,
-                size_t ws_bytes) {
+                size_t ws_bytes, bool stream) {
     RVM_CHECK(layer_ok(L) && x && out && ws && n_tok > 0 && n_tok <= MAX_TOKENS);
-    if (n_tok == 1) return moe_decode(L, x, out, flags, xf, ws, ws_bytes);
+    if (n_tok == 1) return moe_decode(L, x, out, flags, xf, ws, ws_bytes, stream);
     const WsLayout lay = ws_layout(L, n_tok);
     RVM_CHECK(ws_bytes >= lay.total);
     uint8_t *w = (uint8_t *)ws;

@@ -102,14 +102,23 @@ __device__ __forceinline__ float gelu(float x) {
     return 0.5f * x * (1.0f + tanhf_select(inner));
 }
 
-// Loads with the nontemporal hint, for expert weights that one call reads once: they then do not push
-// the router rows and the activations out of the caches.
+// Expert weight loads, with the nontemporal hint when NT (weights read once in a stack of layers:
+// they then do not push the router rows and the activations out of the caches).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 ld_stream(const uint4 *p) {
-    const u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)p);
-    return make_uint4(v.x, v.y, v.z, v.w);
+template <bool NT>
+__device__ __forceinline__ uint4 ld_weights(const uint4 *p) {
+    if constexpr (NT) {
+        const u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)p);
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return *p;
+    }
 }
-__device__ __forceinline__ uint32_t ld_stream(const uint16_t *p) { return __builtin_nontemporal_load(p); }
+template <bool NT>
+__device__ __forceinline__ uint32_t ld_weights(const uint16_t *p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
 
 // One block's term of the reference dot, (sumi as f32) * (d_w * d_x), each product rounded
 // (runtime/src/expert_kernel.rs:158); the reference folds these terms in block order from 0.0.
@@ -362,11 +371,14 @@ int record_event(hipEvent_t e);
 int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, const XForm &xf, uint8_t *ws,
                   const WsLayout &lay, int32_t *ids, float *wts, float *logits, bool select);
 // One decode token (decode.hip) and n_tok tokens (grouped.hip) through the layer with input
-// transform xf; flags carries RVM_EXACT_SELECT.
+// transform xf; flags carries RVM_EXACT_SELECT. stream: the decode kernel loads the expert weights
+// with the nontemporal hint (a stack of layers, whose weights are read once per token and exceed
+// the last-level cache); a single layer called token after token keeps plain loads, so that the
+// experts it uses again can come from that cache.
 int moe_decode(const rvm_layer *L, const float *x, float *out, int flags, const XForm &xf, void *ws,
-               size_t ws_bytes);
+               size_t ws_bytes, bool stream = false);
 int moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int flags, const XForm &xf, void *ws,
-                size_t ws_bytes);
+                size_t ws_bytes, bool stream = false);
 // k_plan; with tiles set it also cuts every group into tiles of up to cap pairs: tiles[0] = count,
 // then (expert, first position in order) per tile, in expert order; tiles2 likewise with cap2.
 int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart,

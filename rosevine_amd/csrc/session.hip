@@ -115,10 +115,10 @@ int rvm_session_eval_range(rvm_session *s, const float *x, float *out, int n_tok
         if (!s->norms.empty()) {
             const rvm_block_norms &nm = s->norms[l];
             const XForm xf{1, nm.eps, nm.router_post, nm.router_scale, nm.expert_scale};
-            rc = moe_forward(L, in, dst, n_tok, flags, xf, s->ws, s->ws_bytes);
+            rc = moe_forward(L, in, dst, n_tok, flags, xf, s->ws, s->ws_bytes, true);
         } else {
             const int f = flags | (l > 0 ? RVM_PRE_NORM : 0);
-            rc = moe_forward(L, in, dst, n_tok, f, xform_of_flags(f, s->eps), s->ws, s->ws_bytes);
+            rc = moe_forward(L, in, dst, n_tok, f, xform_of_flags(f, s->eps), s->ws, s->ws_bytes, true);
         }
         span_mark_after_router(nullptr);
         if (rc) {
