@@ -198,18 +198,15 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void k_select(const double2 *__rest
 // of a wave is token t0 + l, the wave's expert is uniform, and each lane adds the f32 products
 // W_r[e][i] * r[i] of the router input r in element order from -0.0 (runtime/src/ops.rs:321-326),
 // then the bias, so the logits are the reference's bit for bit. 512 tokens x 128 experts are 1024
-// waves, one per SIMD: each fold is a chain of d dependent adds, and the kernel is bound by that
-// chain's VALU issue (a multiply and an add per element) and by the LDS reads of the tokens.
-// The tile's 64 tokens are staged in LDS FKC columns at a time (double-buffered, the next chunk's
-// loads in flight), as the router input (the rms_norm scale and the router's factors applied once
-// per element). Column quad q of token t sits at [q][t ^ (q & 7)], so the coalesced stores (eight
-// quads of one token) and the per-token reads (one quad of 64 tokens) are free of bank conflicts.
-// The wave's router row comes through vector loads at one address for all lanes, 32 columns at a
-// time into a ring of four register sets, three sets ahead of their use: vector loads complete in
-// order, so the wait for a set never waits for the loads behind it (scalar loads would share their
-// counter with the LDS reads and complete out of order). Workgroup g also quantises the Q8_0
-// blocks of the experts' input of tokens g, g + gridDim.x, ... of each staged chunk
-// (runtime/src/ops.rs:95-105).
+// waves, one per SIMD: each fold is a chain of d dependent adds (about 4 ns each on one wave), and
+// the kernel is bound by that chain and by the LDS reads of the tokens. The tile's 64 tokens are
+// staged in LDS FKC columns at a time (double-buffered, the loads of two chunks ahead in flight).
+// Column quad q of token t sits at [q][t ^ (q & 7)], so the coalesced stores (eight quads of one
+// token) and the per-token reads (one quad of 64 tokens) are free of bank conflicts. The workgroup's
+// FW router rows are staged in LDS once; each product is a v_mul_f32_dpp whose row_newbcast operand
+// hands one row element to its 16-lane row (fold_quad2). Without the norm, the workgroups also write
+// the tokens' Q8_0 blocks of the experts' input (runtime/src/ops.rs:95-105), which k_router_prep
+// writes otherwise.
 constexpr int FOLD_MIN_TOKENS = RVM_FOLD_MIN_TOKENS;
 constexpr int FW = 4;     // waves (experts) per workgroup
 constexpr int FKC = 128;  // columns per staged chunk
