@@ -104,7 +104,8 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
     constexpr int R = 16 * MT, NT = W * 64, XP = TileLds<MT, NR, KC, W>::XP;
     constexpr int XU = KC * QK / 16;  // 16-byte pieces of a staged row chunk
     constexpr int XI = (R * XU + NT - 1) / NT, SI = (R * KC + NT - 1) / NT;
-    constexpr int SPL = KC * 16 * NR / 64;  // weight scales per lane per chunk (2, 4 or 8)
+    constexpr int SPL = KC * 16 * NR / 64;  // weight scales per lane per chunk
+    static_assert(NR == 2 && SPL == 2, "two pieces of 16 rows per wave, one dword of scales per lane and chunk");
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nb = width / QK, nch = (nb + KC - 1) / KC;
@@ -163,19 +164,7 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
         }
         // entries j, j+1, ... of the wave's pieces: plane lane 16 (p0 + PS (j / 16)) + j mod 16
         const uint16_t *sp = scl + entry(c * KC + skb) + 16 * p0 + (sj & 15) + 16 * PS * (sj >> 4);
-        if constexpr (SPL == 8) {
-            const uint4 v = *(const uint4 *)sp;
-            wsc[0] = v.x;
-            wsc[1] = v.y;
-            wsc[2] = v.z;
-            wsc[3] = v.w;
-        } else if constexpr (SPL == 4) {
-            const uint2 v = *(const uint2 *)sp;
-            wsc[0] = v.x;
-            wsc[1] = v.y;
-        } else {
-            wsc[0] = *(const uint32_t *)sp;
-        }
+        wsc[0] = *(const uint32_t *)sp;
     };
     auto load_x = [&](int c, uint4 (&xr)[XI], float (&sr)[SI]) {
 #pragma unroll
@@ -211,18 +200,8 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
         for (int kb = 0; kb < KC; ++kb) {
             const int b = c * KC + kb;
             if (b >= nb) break;
-            float dw[NR];
-            if constexpr (NR == 4) {
-                const uint2 v = *(const uint2 *)(wsw + (kb * 16 + m) * NR);
-                dw[0] = h2f((uint16_t)v.x);
-                dw[1] = h2f((uint16_t)(v.x >> 16));
-                dw[2] = h2f((uint16_t)v.y);
-                dw[3] = h2f((uint16_t)(v.y >> 16));
-            } else {
-                const uint32_t v = *(const uint32_t *)(wsw + (kb * 16 + m) * NR);
-                dw[0] = h2f((uint16_t)v);
-                dw[1] = h2f((uint16_t)(v >> 16));
-            }
+            const uint32_t v = *(const uint32_t *)(wsw + (kb * 16 + m) * NR);
+            const float dw[NR] = {h2f((uint16_t)v), h2f((uint16_t)(v >> 16))};
             long a[MT];
             float4 dx[MT];
 #pragma unroll
@@ -281,12 +260,12 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
 // Gate/up for one tile (blockIdx.y) of up to 16 MT pairs of expert e, TW row tiles per workgroup
 // (32 gate rows and the matching 32 up rows each, one RVM_PACK_GATE_UP tile), half a row tile per
 // wave: wave w takes row tile rt = TW blockIdx.x + w / 2, gate rows 16 h + m (piece h = w mod 2) and
-// the matching up rows (piece h + 2). Half-tile waves are twice as many, each half as long, at 112
+// the matching up rows (piece h + 2). Half-tile waves are twice as many, each half as long, at 110
 // VGPRs (four waves per SIMD, against three for whole row tiles at 168): the grid's last partial
 // round of workgroups leaves fewer SIMDs short of waves (512 tokens: 297 -> 275 us per call). A tile
 // of at most 16 pairs (the remainder of an expert's pairs after a full tile) runs the loop of its
 // one occupied m-tile: 16% fewer MFMAs, 11% fewer VALU instructions, the time within the run-to-run
-// spread (at 110 VGPRs the second instance costs no wave).
+// spread (the second instance costs no wave).
 // h = gelu(gate) * up is quantised per pair to one Q8_0 block of 32 (runtime/src/ops.rs:95-105) and
 // stored in the K order of kperm; the block spans both waves' rows, so they exchange their maxima of
 // |h| in LDS (a maximum of non-negative values, the same bits in any order).
