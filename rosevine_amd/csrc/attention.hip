@@ -438,27 +438,8 @@ struct StreamShape {
     static_assert(LDS <= 163840, "LDS");
 };
 
-// s_waitcnt with vmcnt = n and no wait on the other counters (gfx9 encoding)
-constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
 typedef __attribute__((address_space(3))) v2i_t lds_v2i_t;
 
-// Copies to LDS (global_load_lds): lane l's 16 (4) bytes at src go to LDS address lds + 16 l (4 l),
-// lds the same in every lane. Issued through asm so that the compiler, which cannot tell the ring's
-// stages apart, adds no wait for them before LDS reads: the kernel counts them itself (vmcnt).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_copy16(const void *src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "memory", "m0");
-}
-__device__ __forceinline__ void lds_copy4(const void *src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(src), "s"(lds) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p);
-}
 
 __device__ __forceinline__ bf16x8 q8x8_bf16(uint32_t a, uint32_t b) {
     uint32_t k[4];

@@ -444,8 +444,8 @@ __device__ __forceinline__ v4i quad_sums16(uint4 w, uint4 x0, uint4 x1) {
     return s;
 }
 
-// acc[i] = acc[i] + (16 sumi_i as f32) * (d_w * d_x_i / 16), the reference's term (dx holds the
-// four pairs' d_x / 16).
+// acc[i] = acc[i] + (16 sumi_i as f32) * (d_w / 16 * d_x_i), the reference's term (dw holds d_w / 16,
+// dx the four pairs' d_x: d_w * d_x is exact in f32 for binary16 scales, and so is its sixteenth).
 __device__ __forceinline__ void quad_fold(float (&acc)[4], v4i s16, float dw, float4 dx) {
     acc[0] = acc[0] + (float)s16[0] * (dw * dx.x);
     acc[1] = acc[1] + (float)s16[1] * (dw * dx.y);
@@ -454,30 +454,30 @@ __device__ __forceinline__ void quad_fold(float (&acc)[4], v4i s16, float dw, fl
 }
 
 // The wave's LDS region: the four pairs' activation rows (K order of kperm) at a pitch of
-// width + 16 bytes, so that the four rows start on different LDS banks, then their block scales
-// divided by 16, [block][pair].
+// width + 16 bytes, so that the four rows start on different LDS banks, then their block scales,
+// [block][pair].
 __host__ __device__ constexpr int quad_pitch(int width) { return width + 16; }
 __host__ __device__ constexpr int quad_lds_bytes(int width) { return 4 * quad_pitch(width) + 4 * (width / QK) * 4; }
 
 // Copies the rows src_r = src + row_r * width (and scales ssrc + row_r * nb) of the wave's four
-// pairs into its LDS region; row_r comes from lane r of rowv.
+// pairs into its LDS region; row_r comes from lane r of rowv. The copies go from memory straight
+// to LDS (64 pieces of 16 bytes of one row, or 64 scales, per instruction), all issued before one
+// wait: one memory round trip, where register copies had one per piece.
 __device__ __forceinline__ void stage_quad_rows(const int8_t *__restrict__ src, const float *__restrict__ ssrc,
                                                 int rowv, int width, uint8_t *lds) {
     const int lane = threadIdx.x & 63, nb = width / QK, pcs = width / 16, P = quad_pitch(width);
-    int row[4];
+    const uint32_t base = lds_addr(lds);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) row[r] = __shfl(rowv, r);
-    for (int p = lane; p < 4 * pcs; p += 64) {
-        const int r = p / pcs, c = p - r * pcs;
-        const int sr = r == 0 ? row[0] : (r == 1 ? row[1] : (r == 2 ? row[2] : row[3]));
-        *(uint4 *)(lds + r * P + c * 16) = *(const uint4 *)(src + (size_t)sr * width + c * 16);
+    for (int r = 0; r < 4; ++r) {
+        const int8_t *rowp = src + (size_t)__builtin_amdgcn_readfirstlane(__shfl(rowv, r)) * width;
+        for (int c0 = 0; c0 < pcs; c0 += 64)
+            if (c0 + lane < pcs) lds_copy16(rowp + (size_t)(c0 + lane) * 16, base + r * P + c0 * 16);
     }
-    float *sl = (float *)(lds + 4 * P);
-    for (int p = lane; p < 4 * nb; p += 64) {
-        const int r = p / nb, b = p - r * nb;
-        const int sr = r == 0 ? row[0] : (r == 1 ? row[1] : (r == 2 ? row[2] : row[3]));
-        sl[4 * b + r] = ssrc[(size_t)sr * nb + b] * 0.0625f;  // d_x / 16
-    }
+    // scale q = 4 b + r at [b][r]: lane l of a 64-scale copy is pair l mod 4
+    const float *srow = ssrc + (size_t)__shfl(rowv, lane & 3) * nb;
+    for (int q0 = 0; q0 < 4 * nb; q0 += 64)
+        if (q0 + lane < 4 * nb) lds_copy4(srow + (q0 + lane) / 4, base + 4 * P + q0 * 4);
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     wave_lds_sync();
 }
 
@@ -501,7 +501,7 @@ __device__ __forceinline__ void quad_row_sums(const uint4 *__restrict__ nib, con
     };
     auto compute = [&](int u, int b) {
         const uint4 x0 = *(const uint4 *)(xl + 32 * b), x1 = *(const uint4 *)(xl + 32 * b + 16);
-        quad_fold(acc, quad_sums16(w[u], x0, x1), h2f((uint16_t)s[u]), sl[b]);
+        quad_fold(acc, quad_sums16(w[u], x0, x1), h2f((uint16_t)s[u]) * 0.0625f, sl[b]);
     };
     // The first round only loads (and then stages the activation rows, their loads behind the
     // weights'): it is the same code as the later rounds, so the loads are issued in the same order

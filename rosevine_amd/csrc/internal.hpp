@@ -120,6 +120,26 @@ __device__ __forceinline__ uint32_t ld_weights(const uint16_t *p) {
     else return *p;
 }
 
+// s_waitcnt with vmcnt = n and no wait on the other counters (gfx9 encoding)
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Copies to LDS (global_load_lds): lane l's 16 (4) bytes at src go to LDS address lds + 16 l (4 l),
+// lds the same in every lane. Issued through asm, so the compiler adds no wait for them before LDS
+// reads: the kernel waits for them itself (vmcnt).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_copy16(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy4(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p);
+}
+
 // One block's term of the reference dot, (sumi as f32) * (d_w * d_x), each product rounded
 // (runtime/src/expert_kernel.rs:158); the reference folds these terms in block order from 0.0.
 __device__ __forceinline__ float block_term(int sumi, float dw, float dx) { return (float)sumi * (dw * dx); }
