@@ -42,9 +42,9 @@ constexpr int MW = 4;  // waves (row tiles) per workgroup
 // (the small-batch kernels, where a popular expert has several tiles; the arithmetic-bound batched
 // kernels keep every XCD busy instead).
 inline int xcd_rows(int n) { return (n + 7) & ~7; }
-// K blocks per chunk (a template parameter of the tile loop; 8 measured slower for one m-tile)
-template <int MT>
-constexpr int chunk_blocks() { return 4; }
+// K blocks per chunk of the tile loop: 4 for gate/up (d is a multiple of 256, so d / 32 blocks
+// are whole chunks; 8 measured slower for one m-tile), 2 for down (ff is a multiple of 64)
+constexpr int GU_KC = 4, DN_KC = 2;
 
 // 16 times the int8 weights of one K slice of a packed Q4_0 entry's dword g (bytes 4g .. 4g+3,
 // each nibble the 4-bit two's complement weight; byte k holds elements 4g + k in its low nibble and
@@ -88,27 +88,32 @@ struct TileLds {
 
 // The block sums of one tile: rows of the wave's row tile (entry groups tb .. tb+S-1, NR pieces of
 // 16 plane lanes, pieces p0, p0 + PS, ..., wave-uniform; block b uses group b mod S at lane offset
-// 32 (b / S)) against the tile's R
-// activation rows (K = width, nb = width / 32 blocks). acc[mt][r][i] is the output of pair
-// 16 mt + 4 g + i and plane lane 16 r + m, for lane = 16 g + m. Only the first LIVE m-tiles are
-// computed (the others hold no pair; their acc stays 0). All waves take part in the staging and
-// barriers; waves without a row tile (active false) skip the weights and MFMAs.
-template <int MT, int NR, int KC, int LIVE, int W = MW, int PS = 1>
+// 32 (b / S) when HALVES, group b otherwise) against the tile's R activation rows (K = width,
+// nb = width / 32 blocks, a multiple of KC; src holds rows rows of width bytes, ssrc their nb block
+// scales). acc[mt][r][i] is the output of pair 16 mt + 4 g + i and plane lane 16 r + m, for
+// lane = 16 g + m. Only the first LIVE m-tiles are computed (the others hold no pair; their acc
+// stays 0). All waves take part in the staging and barriers; waves without a row tile (active
+// false) skip the MFMAs.
+template <int MT, int NR, int KC, int LIVE, bool HALVES, int W = MW, int PS = 1>
 __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const uint16_t *__restrict__ scl,
                                           size_t tb, int S, bool active, const int8_t *__restrict__ src,
-                                          const float *__restrict__ ssrc, int width, TileLds<MT, NR, KC, W> &sh,
-                                          float (&acc)[MT][NR][4], int p0 = 0) {
-    // Every global load below is issued unconditionally (addresses clamped into the buffers, the
-    // values selected when stored), so that the compiler can count the loads in flight and wait
-    // for exactly the ones it needs: the next chunk's loads stay outstanding while this one runs.
+                                          const float *__restrict__ ssrc, int width, int rows,
+                                          TileLds<MT, NR, KC, W> &sh, float (&acc)[MT][NR][4], int p0 = 0) {
+    // Every load goes through a buffer descriptor: the wave-uniform part of its offset (the chunk's)
+    // sits in a scalar register, so the loads cost no vector address arithmetic, and an empty tile
+    // place's loads take an offset past the end of the buffer, which reads 0. The loads of the chunk
+    // after the last reload the last chunk (unused), so every load is issued unconditionally and the
+    // compiler can count the loads in flight and wait for exactly the ones it needs: the next
+    // chunk's loads stay outstanding while this one runs. Whole chunks only (no exit inside the
+    // unrolled block loop, whose join would copy every accumulator).
     constexpr int R = 16 * MT, NT = W * 64, XP = TileLds<MT, NR, KC, W>::XP;
     constexpr int XU = KC * QK / 16;  // 16-byte pieces of a staged row chunk
     constexpr int XI = (R * XU + NT - 1) / NT, SI = (R * KC + NT - 1) / NT;
     constexpr int SPL = KC * 16 * NR / 64;  // weight scales per lane per chunk
-    static_assert(NR == 2 && SPL == 2, "two pieces of 16 rows per wave, one dword of scales per lane and chunk");
+    static_assert(NR == 2 && (SPL == 1 || SPL == 2), "two pieces of 16 rows per wave, at most one dword of scales per lane and chunk");
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nb = width / QK, nch = (nb + KC - 1) / KC;
+    const int nb = width / QK, nch = nb / KC;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -116,90 +121,90 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[mt][r][i] = 0.0f;
 
-    auto entry = [&](int b) {  // first plane entry of block b (clamped to the last block)
-        b = min(b, nb - 1);
-        const int half = b >= S ? 1 : 0;
-        return (tb + (size_t)(b - half * S)) * 64 + 32 * half;
+    // the row tile's plane entries (S groups of 64) and their scales; the activation rows and scales
+    const __amdgpu_buffer_rsrc_t wres = buffer_rsrc(nib + tb * 1024, (uint32_t)S * 1024u);
+    const __amdgpu_buffer_rsrc_t sres = buffer_rsrc(scl + tb * 64, (uint32_t)S * 128u);
+    const __amdgpu_buffer_rsrc_t xres = buffer_rsrc(src, (uint32_t)rows * (uint32_t)width);
+    const __amdgpu_buffer_rsrc_t xsres = buffer_rsrc(ssrc, (uint32_t)rows * (uint32_t)nb * 4u);
+    constexpr uint32_t EMPTY = 0x80000000u;  // an offset past the end of every buffer here
+    auto eoff = [&](int b) {  // entry of block b from the row tile's first
+        if constexpr (HALVES) {
+            const int half = b >= S ? 1 : 0;
+            return (b - half * S) * 64 + 32 * half;
+        } else {
+            return b * 64;
+        }
     };
     // this lane's share of a chunk's weight scales: block kb = lane / (64 / KC), entries
-    // j .. j+SPL-1 of it
+    // j .. j+SPL-1 of it, plane lane 16 (p0 + PS (j / 16)) + j mod 16
     constexpr int LPB = 64 / KC;
     const int skb = lane / LPB, sj = (lane % LPB) * SPL;
+    const int sjl = 16 * p0 + (sj & 15) + 16 * PS * (sj >> 4);
     // this thread's staging items, fixed over the chunks: activation piece q of tile place xrow[k],
-    // and the scale of place srow[k] at chunk block skbx[k]
-    // (32-bit offsets from the scalar bases src and ssrc: the rows are at most 65535 x 8 pairs of
-    // 1024 bytes, or tokens of 4096)
-    uint32_t xsrc[XI];
-    int xq[XI], xdst[XI];
-    bool xok[XI];
+    // and the scale of place srow[k] at chunk block skbx[k] (offsets at chunk 0)
+    uint32_t xoff[XI];
+    int xdst[XI];
 #pragma unroll
     for (int k = 0; k < XI; ++k) {
         const int i = threadIdx.x + k * NT, ii = min(i, R * XU - 1);
         const int row = ii / XU, q = ii - row * XU, from = sh.row_of[row];
-        xok[k] = i < R * XU && from >= 0;
-        xsrc[k] = (uint32_t)(from >= 0 ? from : 0) * (uint32_t)width;
-        xq[k] = q * 16;
+        xoff[k] = from >= 0 ? (uint32_t)from * (uint32_t)width + (uint32_t)(q * 16) : EMPTY;
         xdst[k] = i < R * XU ? row * XP + q * 16 : -1;
     }
-    uint32_t ssp[SI];
-    int skbx[SI];
-    bool sok[SI];
+    uint32_t soffx[SI];
+    int sdst[SI];
 #pragma unroll
     for (int k = 0; k < SI; ++k) {
         const int i = threadIdx.x + k * NT, ii = min(i, R * KC - 1);
         const int kb = ii / R, row = ii - kb * R, from = sh.row_of[row];
-        sok[k] = i < R * KC && from >= 0;
-        ssp[k] = (uint32_t)(from >= 0 ? from : 0) * (uint32_t)nb;
-        skbx[k] = i < R * KC ? kb : -1;
+        soffx[k] = from >= 0 ? ((uint32_t)from * (uint32_t)nb + (uint32_t)kb) * 4u : EMPTY;
+        sdst[k] = i < R * KC ? i : -1;  // [block][row]
     }
 
     const int loff = m * 16 + 4 * g;  // this lane's byte in a piece of 16 plane entries
-    constexpr int SW = SPL / 2;  // dwords of weight scales per lane per chunk
-    auto load_w = [&](int c, uint32_t (&wn)[KC][NR], uint32_t (&wsc)[SW]) {
+    auto load_w = [&](int c, uint32_t (&wn)[KC][NR], uint32_t &wsc) {
+        const int cc = min(c, nch - 1);
 #pragma unroll
         for (int kb = 0; kb < KC; ++kb) {
-            const uint8_t *pb = nib + entry(c * KC + kb) * 16;  // wave-uniform: a scalar base
+            const uint32_t so = (uint32_t)eoff(cc * KC + kb) * 16u;  // wave-uniform
 #pragma unroll
-            for (int r = 0; r < NR; ++r) wn[kb][r] = *(const uint32_t *)(pb + (256 * (p0 + PS * r) + loff));
+            for (int r = 0; r < NR; ++r) wn[kb][r] = buffer_load_u32(wres, (uint32_t)(256 * (p0 + PS * r) + loff), so);
         }
-        // entries j, j+1, ... of the wave's pieces: plane lane 16 (p0 + PS (j / 16)) + j mod 16
-        const uint16_t *sp = scl + entry(c * KC + skb) + 16 * p0 + (sj & 15) + 16 * PS * (sj >> 4);
-        wsc[0] = *(const uint32_t *)sp;
+        if constexpr (HALVES) {
+            const uint32_t vo = (uint32_t)(eoff(cc * KC + skb) + sjl) * 2u;
+            wsc = SPL == 2 ? buffer_load_u32(sres, vo, 0) : buffer_load_u16(sres, vo, 0);
+        } else {
+            const uint32_t vo = (uint32_t)(skb * 64 + sjl) * 2u, so = (uint32_t)(cc * KC) * 128u;
+            wsc = SPL == 2 ? buffer_load_u32(sres, vo, so) : buffer_load_u16(sres, vo, so);
+        }
     };
     auto load_x = [&](int c, uint4 (&xr)[XI], float (&sr)[SI]) {
+        const uint32_t cc = (uint32_t)min(c, nch - 1);
+#pragma unroll
+        for (int k = 0; k < XI; ++k) xr[k] = buffer_load_u4(xres, xoff[k], cc * (KC * QK));
+#pragma unroll
+        for (int k = 0; k < SI; ++k) sr[k] = buffer_load_f32(xsres, soffx[k], cc * (KC * 4));
+    };
+    auto store_x = [&](int buf, const uint4 (&xr)[XI], const float (&sr)[SI]) {
 #pragma unroll
         for (int k = 0; k < XI; ++k)
-            xr[k] = *(const uint4 *)(src + (xsrc[k] + (uint32_t)min(c * KC * QK + xq[k], width - 16)));
+            if (xdst[k] >= 0) *(uint4 *)(sh.xs[buf] + xdst[k]) = xr[k];
 #pragma unroll
-        for (int k = 0; k < SI; ++k) sr[k] = ssrc[ssp[k] + (uint32_t)min(c * KC + max(skbx[k], 0), nb - 1)];
+        for (int k = 0; k < SI; ++k)
+            if (sdst[k] >= 0) sh.ss[buf][sdst[k]] = sr[k] * 0.0625f;  // d_x / 16
     };
-    auto store_x = [&](int c, int buf, const uint4 (&xr)[XI], const float (&sr)[SI]) {
-#pragma unroll
-        for (int k = 0; k < XI; ++k) {
-            const bool ok = xok[k] && c * KC * QK + xq[k] < width;
-            if (xdst[k] >= 0) *(uint4 *)(sh.xs[buf] + xdst[k]) = ok ? xr[k] : make_uint4(0u, 0u, 0u, 0u);
-        }
-#pragma unroll
-        for (int k = 0; k < SI; ++k) {
-            const bool ok = sok[k] && c * KC + skbx[k] < nb;
-            if (skbx[k] >= 0) sh.ss[buf][threadIdx.x + k * NT] = ok ? sr[k] * 0.0625f : 0.0f;  // d_x / 16
-        }
-    };
-    auto compute = [&](int c, int buf, const uint32_t (&wn)[KC][NR], const uint32_t (&wsc)[SW]) {
+    auto compute = [&](int buf, const uint32_t (&wn)[KC][NR], uint32_t wsc) {
         if (!active) return;
         // the chunk's weight scales to [block][m][piece] in this wave's LDS
         uint16_t *wsw = sh.ws[w];
 #pragma unroll
         for (int k = 0; k < SPL; ++k) {
             const int j = sj + k;
-            const uint32_t v = wsc[k >> 1] >> ((k & 1) * 16);
-            wsw[(skb * 16 + (j & 15)) * NR + (j >> 4)] = (uint16_t)v;
+            wsw[(skb * 16 + (j & 15)) * NR + (j >> 4)] = (uint16_t)(wsc >> (16 * k));
         }
         wave_lds_sync();
 #pragma unroll
         for (int kb = 0; kb < KC; ++kb) {
-            const int b = c * KC + kb;
-            if (b >= nb) break;
             const uint32_t v = *(const uint32_t *)(wsw + (kb * 16 + m) * NR);
             const float dw[NR] = {h2f((uint16_t)v), h2f((uint16_t)(v >> 16))};
             long a[MT];
@@ -227,31 +232,30 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
     };
 
     uint32_t wn0[KC][NR], wn1[KC][NR];
-    uint32_t ws0[SW], ws1[SW];
+    uint32_t ws0, ws1;
     uint4 xr[XI];
     float sr[SI];
     load_x(0, xr, sr);
     load_w(0, wn0, ws0);
-    store_x(0, 0, xr, sr);
+    store_x(0, xr, sr);
     __syncthreads();
     for (int c = 0; c < nch; c += 2) {
         {
             const bool more = c + 1 < nch;
             // staging loads first: store_x waits for them, and the in-order load counter then
-            // leaves the weight loads behind them in flight; past the end both reload the last
-            // block, unused
+            // leaves the weight loads behind them in flight
             load_x(c + 1, xr, sr);
             load_w(c + 1, wn1, ws1);
-            compute(c, 0, wn0, ws0);
-            if (more) store_x(c + 1, 1, xr, sr);
+            compute(0, wn0, ws0);
+            if (more) store_x(1, xr, sr);
             __syncthreads();
         }
         if (c + 1 < nch) {
             const bool more = c + 2 < nch;
             load_x(c + 2, xr, sr);
             load_w(c + 2, wn0, ws0);
-            compute(c + 1, 1, wn1, ws1);
-            if (more) store_x(c + 2, 0, xr, sr);
+            compute(1, wn1, ws1);
+            if (more) store_x(0, xr, sr);
             __syncthreads();
         }
     }
@@ -277,8 +281,9 @@ __global__ __launch_bounds__(128 * TW) void k_gateup_mfma(const uint8_t *__restr
                                                           const int32_t *__restrict__ order,
                                                           const int8_t *__restrict__ xq8,
                                                           const float *__restrict__ xsc, int8_t *__restrict__ hq8,
-                                                          float *__restrict__ hsc, int d, int ff, int top_k) {
-    constexpr int R = 16 * MT, KC = chunk_blocks<MT>();
+                                                          float *__restrict__ hsc, int d, int ff, int top_k,
+                                                          int n_tok) {
+    constexpr int R = 16 * MT, KC = GU_KC;
     __shared__ TileLds<MT, 2, KC, 2 * TW> sh;
     __shared__ float hmax[2 * TW][MT][4][4];  // [wave][m-tile][i][g]: max of |h| over the wave's 16 rows
     const int tile = blockIdx.y;
@@ -294,9 +299,9 @@ __global__ __launch_bounds__(128 * TW) void k_gateup_mfma(const uint8_t *__restr
     float acc[MT][2][4];
     const size_t tb = ((size_t)e * Tg + (active ? rt : 0)) * nb;
     if (MT > 1 && cnt <= 16)  // a tile of at most 16 pairs runs the loop of its one occupied m-tile
-        tile_sums<MT, 2, KC, 1, 2 * TW, 2>(nib, scl, tb, nb, active, xq8, xsc, d, sh, acc, h);
+        tile_sums<MT, 2, KC, 1, false, 2 * TW, 2>(nib, scl, tb, nb, active, xq8, xsc, d, n_tok, sh, acc, h);
     else
-        tile_sums<MT, 2, KC, MT, 2 * TW, 2>(nib, scl, tb, nb, active, xq8, xsc, d, sh, acc, h);
+        tile_sums<MT, 2, KC, MT, false, 2 * TW, 2>(nib, scl, tb, nb, active, xq8, xsc, d, n_tok, sh, acc, h);
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
     float hv[MT][4];
 #pragma unroll
@@ -339,8 +344,8 @@ __global__ __launch_bounds__(MW * 64) void k_down_mfma(const uint8_t *__restrict
                                                        const int32_t *__restrict__ tiles,
                                                        const int32_t *__restrict__ gstart,
                                                        const int8_t *__restrict__ hq8, const float *__restrict__ hsc,
-                                                       float *__restrict__ y, int d, int ff) {
-    constexpr int R = 16 * MT, KC = chunk_blocks<MT>();
+                                                       float *__restrict__ y, int d, int ff, int n_pairs) {
+    constexpr int R = 16 * MT, KC = DN_KC;
     __shared__ TileLds<MT, 2, KC> sh;
     const int tile = blockIdx.y;
     if (tile >= tiles[0]) return;
@@ -356,11 +361,11 @@ __global__ __launch_bounds__(MW * 64) void k_down_mfma(const uint8_t *__restrict
     // kernel, measured slower here: 282 against 276.5 us for 512 tokens)
     const size_t tb = ((size_t)e * Td + (active ? rt : 0)) * Sd;
     if (MT > 1 && cnt <= 16)
-        tile_sums<MT, 2, KC, 1>(nib, scl, tb, Sd, active, hq8, hsc, ff, sh, acc);
+        tile_sums<MT, 2, KC, 1, true>(nib, scl, tb, Sd, active, hq8, hsc, ff, n_pairs, sh, acc);
     else if (MT > 2 && cnt <= 32)
-        tile_sums<MT, 2, KC, (MT > 2 ? 2 : MT)>(nib, scl, tb, Sd, active, hq8, hsc, ff, sh, acc);
+        tile_sums<MT, 2, KC, (MT > 2 ? 2 : MT), true>(nib, scl, tb, Sd, active, hq8, hsc, ff, n_pairs, sh, acc);
     else
-        tile_sums<MT, 2, KC, MT>(nib, scl, tb, Sd, active, hq8, hsc, ff, sh, acc);
+        tile_sums<MT, 2, KC, MT, true>(nib, scl, tb, Sd, active, hq8, hsc, ff, n_pairs, sh, acc);
     if (!active) return;
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -665,7 +670,7 @@ int launch_experts(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &la
     hipLaunchKernelGGL(gkern, dim3(grid_blocks(L->ff / 32, TW), nt), dim3(128 * TW), 0, cur_stream(), gnib, gscl, tiles,
                        gstart, (const int32_t *)(w + lay.order), (const int8_t *)(w + lay.xq8),
                        (const float *)(w + lay.xsc), (int8_t *)(w + lay.hq8), (float *)(w + lay.hsc), L->d, L->ff,
-                       L->top_k);
+                       L->top_k, n_tok);
     int rc = launched();
     if (rc) return rc;
     const size_t dn_entries = (size_t)L->n_exp * L->d * (L->ff / QK);
@@ -673,7 +678,7 @@ int launch_experts(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &la
     const uint16_t *dscl = (const uint16_t *)(dnib + dn_entries * 16);
     hipLaunchKernelGGL(k_down_mfma<MD>, dim3(grid_blocks(L->d / 32, MW), nd), dim3(MW * 64), 0, cur_stream(), dnib,
                        dscl, tiles2, gstart, (const int8_t *)(w + lay.hq8), (const float *)(w + lay.hsc),
-                       (float *)(w + lay.y), L->d, L->ff);
+                       (float *)(w + lay.y), L->d, L->ff, n_tok * L->top_k);
     return launched();
 }
 

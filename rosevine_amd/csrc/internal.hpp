@@ -140,6 +140,36 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p);
 }
 
+// A raw buffer descriptor over [p, p + bytes): loads through it take an SGPR base, a 32-bit VGPR
+// offset and a wave-uniform offset, and read 0 at or past the end (no fault).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+typedef uint32_t u32v4 __attribute__((__vector_size__(16)));
+// The whole vector is copied: a bit cast of one element of a vector type reads element 0's storage
+// with this compiler.
+__device__ __forceinline__ float4 buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const u32v4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    float4 f;
+    __builtin_memcpy(&f, &v, 16);
+    return f;
+}
+__device__ __forceinline__ uint4 buffer_load_u4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const u32v4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    uint4 u;
+    __builtin_memcpy(&u, &v, 16);
+    return u;
+}
+__device__ __forceinline__ uint32_t buffer_load_u32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ uint32_t buffer_load_u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+}
+
 // One block's term of the reference dot, (sumi as f32) * (d_w * d_x), each product rounded
 // (runtime/src/expert_kernel.rs:158); the reference folds these terms in block order from 0.0.
 __device__ __forceinline__ float block_term(int sumi, float dw, float dx) { return (float)sumi * (dw * dx); }

@@ -272,21 +272,6 @@ __global__ __launch_bounds__(256) void k_router_prep(const float *__restrict__ x
     }
 }
 
-// A raw buffer descriptor over [p, p + bytes): loads through it take an SGPR base, a 32-bit VGPR
-// offset and an immediate, and read 0 past the end.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
-}
-typedef uint32_t u32v4 __attribute__((__vector_size__(16)));
-// The whole vector is copied: a bit cast of one element of a vector type reads element 0's storage
-// with this compiler.
-__device__ __forceinline__ float4 buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    const u32v4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
-    float4 f;
-    __builtin_memcpy(&f, &v, 16);
-    return f;
-}
-
 // Quads MA and MB of a 64-column row block: columns 4M .. 4M+3 sit in lane M of each row of 16
 // lanes (w.x .. w.w). Each is handed to every lane by a DPP row broadcast inside the multiply
 // (v_mul_f32_dpp row_newbcast: the plain f32 product, rounded) and added to this lane's fold in
