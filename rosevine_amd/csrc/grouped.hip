@@ -82,7 +82,7 @@ struct TileLds {
     static constexpr int R = 16 * MT, XP = KC * QK + 16;  // row pitch: conflict-free 8-byte reads
     alignas(16) int8_t xs[2][R * XP];           // activation rows of the chunk
     alignas(16) float ss[2][KC * R];            // their block scales, [block][row]
-    alignas(16) uint16_t ws[W][KC * 16 * NR];   // per wave: weight scales, [block][m][piece]
+    alignas(16) float ws[W][KC * 16 * NR];      // per wave: weight scales, [block][m][piece]
     int row_of[R];                              // source row of each tile place, -1 when empty
 };
 
@@ -195,18 +195,18 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
     };
     auto compute = [&](int buf, const uint32_t (&wn)[KC][NR], uint32_t wsc) {
         if (!active) return;
-        // the chunk's weight scales to [block][m][piece] in this wave's LDS
-        uint16_t *wsw = sh.ws[w];
+        // the chunk's weight scales as f32 to [block][m][piece] in this wave's LDS
+        float *wsw = sh.ws[w];
 #pragma unroll
         for (int k = 0; k < SPL; ++k) {
             const int j = sj + k;
-            wsw[(skb * 16 + (j & 15)) * NR + (j >> 4)] = (uint16_t)(wsc >> (16 * k));
+            wsw[(skb * 16 + (j & 15)) * NR + (j >> 4)] = h2f((uint16_t)(wsc >> (16 * k)));
         }
         wave_lds_sync();
 #pragma unroll
         for (int kb = 0; kb < KC; ++kb) {
-            const uint32_t v = *(const uint32_t *)(wsw + (kb * 16 + m) * NR);
-            const float dw[NR] = {h2f((uint16_t)v), h2f((uint16_t)(v >> 16))};
+            const float2 v = *(const float2 *)(wsw + (kb * 16 + m) * NR);
+            const float dw[NR] = {v.x, v.y};
             long a[MT];
             float4 dx[MT];
 #pragma unroll
@@ -261,6 +261,12 @@ __device__ __forceinline__ void tile_sums(const uint8_t *__restrict__ nib, const
     }
 }
 
+// The tile's pair at place 16 mt + 4 g + i (MFMA row 4 g + i of m-tile mt, output register i of lane
+// group g): pairs fill register (mt, i) of all four lane groups before the next, so a tile of cnt
+// pairs occupies the first ceil(cnt / 4) registers and the epilogue skips the others (the pairs of
+// one register are the same MFMA rows for every lane, so the skip is wave-uniform).
+__device__ __forceinline__ int place_pair(int mt, int g, int i) { return 4 * (4 * mt + i) + g; }
+
 // Gate/up for one tile (blockIdx.y) of up to 16 MT pairs of expert e, TW row tiles per workgroup
 // (32 gate rows and the matching 32 up rows each, one RVM_PACK_GATE_UP tile), half a row tile per
 // wave: wave w takes row tile rt = TW blockIdx.x + w / 2, gate rows 16 h + m (piece h = w mod 2) and
@@ -291,7 +297,10 @@ __global__ __launch_bounds__(128 * TW) void k_gateup_mfma(const uint8_t *__restr
     const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
     const int cnt = min(R, gstart[e + 1] - k0);
     const int nb = d / QK, Tg = ff / 32;
-    if (threadIdx.x < R) sh.row_of[threadIdx.x] = (int)threadIdx.x < cnt ? order[k0 + threadIdx.x] / top_k : -1;
+    if (threadIdx.x < R) {  // tile place 16 mt + 4 g + i holds pair place_pair(...) of the tile
+        const int p = threadIdx.x, pr = place_pair(p >> 4, (p >> 2) & 3, p & 3);
+        sh.row_of[p] = pr < cnt ? order[k0 + pr] / top_k : -1;
+    }
     __syncthreads();
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = wv & 1;
     const int rt = blockIdx.x * TW + (wv >> 1);
@@ -306,9 +315,9 @@ __global__ __launch_bounds__(128 * TW) void k_gateup_mfma(const uint8_t *__restr
     float hv[MT][4];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        if (mt * 16 >= cnt) break;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            if (place_pair(mt, 0, i) >= cnt) break;  // wave-uniform: no pair in this register
             hv[mt][i] = gelu(acc[mt][0][i]) * acc[mt][1][i];
             const float mx = row16_max(fmaxf(0.0f, fabsf(hv[mt][i])));
             if (m == 0) hmax[wv][mt][i][g] = mx;
@@ -318,14 +327,14 @@ __global__ __launch_bounds__(128 * TW) void k_gateup_mfma(const uint8_t *__restr
     if (!active) return;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        if (mt * 16 >= cnt) break;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            if (place_pair(mt, 0, i) >= cnt) break;
             const float amax = fmaxf(hmax[wv & ~1][mt][i][g], hmax[wv | 1][mt][i][g]);
             const float dq = amax / 127.0f;
             const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
             const int q = sat_i8(roundf(hv[mt][i] * id));
-            const int pr = mt * 16 + 4 * g + i;
+            const int pr = place_pair(mt, g, i);
             if (pr < cnt) {
                 int8_t *hrow = hq8 + (size_t)(k0 + pr) * ff + rt * QK;
                 hrow[kperm(16 * h + m)] = (int8_t)q;

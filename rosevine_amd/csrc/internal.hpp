@@ -430,7 +430,8 @@ int moe_decode(const rvm_layer *L, const float *x, float *out, int flags, const 
 int moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int flags, const XForm &xf, void *ws,
                 size_t ws_bytes, bool stream = false);
 // k_plan; with tiles set it also cuts every group into tiles of up to cap pairs: tiles[0] = count,
-// then (expert, first position in order) per tile, in expert order; tiles2 likewise with cap2.
+// then (expert, first position in order) per tile, the tiles with more m-tiles of 16 pairs first
+// and in expert order within each such class; tiles2 likewise with cap2.
 int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart,
                 int32_t *tiles, int cap, int32_t *tiles2 = nullptr, int cap2 = 0);
 

@@ -491,6 +491,41 @@ __device__ __forceinline__ void plan_load(const int32_t *__restrict__ ids, int b
         ev[r] = i < hi ? ids[i] : -1;
     }
 }
+// Tile classes: a tile of n pairs has class min(PLAN_NC, ceil(n / 16)) - 1 (its m-tiles of 16 pairs).
+// The tiles are listed class by class, the most m-tiles first, and by expert within a class: the
+// batched kernels' workgroups start in grid order, so the longest tiles start first and the
+// remainder tiles, which run fewer m-tiles, fill the end of the grid.
+constexpr int PLAN_NC = 3;
+__device__ __forceinline__ int tile_class(int n) { return min(PLAN_NC, (n + 15) / 16) - 1; }
+// Adds the tiles of a group of n pairs (tiles of up to cap) to the per-class counts.
+__device__ __forceinline__ void tile_counts(int n, int cap, int (&cnt)[PLAN_NC]) {
+    const int full = n / cap, rem = n - full * cap;
+    const int kf = tile_class(cap), kr = rem ? tile_class(rem) : -1;
+#pragma unroll
+    for (int k = 0; k < PLAN_NC; ++k) cnt[k] += (k == kf ? full : 0) + (k == kr ? 1 : 0);
+}
+// Writes the tiles (expert, first position in order) of expert e's group of n pairs at run: full
+// tiles of cap pairs, then the remainder, each at the next place of its class (pos).
+__device__ __forceinline__ void put_tiles(int32_t *__restrict__ tl, int cap, int e, int n, int run,
+                                          int (&pos)[PLAN_NC]) {
+    const int full = n / cap, rem = n - full * cap;
+    const int kf = tile_class(cap), kr = rem ? tile_class(rem) : -1;
+#pragma unroll
+    for (int k = 0; k < PLAN_NC; ++k) {
+        if (k == kf)
+            for (int q = 0; q < full; ++q) {
+                tl[1 + 2 * pos[k]] = e;
+                tl[2 + 2 * pos[k]] = run + q * cap;
+                ++pos[k];
+            }
+        if (k == kr) {
+            tl[1 + 2 * pos[k]] = e;
+            tl[2 + 2 * pos[k]] = run + full * cap;
+            ++pos[k];
+        }
+    }
+}
+
 __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, int n, int n_exp,
                                                int32_t *__restrict__ order, int32_t *__restrict__ pos_of,
                                                int32_t *__restrict__ gstart, int32_t *__restrict__ tiles, int cap,
@@ -518,54 +553,62 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
         tot[threadIdx.x] = s;
     }
     __syncthreads();
-    if (w == 0) {  // exclusive scans of the group sizes and of their tile counts, 4 experts a lane
+    if (w == 0) {  // exclusive scans of the group sizes and of their tile counts by class, 4 experts a lane
         const int cp2 = tiles2 ? cap2 : 1;
-        int c[4], t[4], t2[4], cs = 0, ts = 0, ts2 = 0;
+        int c[4], cs = 0, s1[PLAN_NC], s2[PLAN_NC];
+#pragma unroll
+        for (int k = 0; k < PLAN_NC; ++k) s1[k] = s2[k] = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int e = 4 * lane + k;
             c[k] = e < n_exp ? tot[e] : 0;
-            t[k] = (c[k] + cap - 1) / cap;
-            t2[k] = (c[k] + cp2 - 1) / cp2;
             cs += c[k];
-            ts += t[k];
-            ts2 += t2[k];
+            tile_counts(c[k], cap, s1);
+            tile_counts(c[k], cp2, s2);
         }
-        int ic = cs, it = ts, it2 = ts2;
+        int ic = cs, i1[PLAN_NC], i2[PLAN_NC];
+#pragma unroll
+        for (int k = 0; k < PLAN_NC; ++k) {
+            i1[k] = s1[k];
+            i2[k] = s2[k];
+        }
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            const int nc = __shfl_up(ic, o), nt = __shfl_up(it, o), nt2 = __shfl_up(it2, o);
-            if (lane >= o) {
-                ic += nc;
-                it += nt;
-                it2 += nt2;
+            const int nc = __shfl_up(ic, o);
+            if (lane >= o) ic += nc;
+#pragma unroll
+            for (int k = 0; k < PLAN_NC; ++k) {
+                const int n1 = __shfl_up(i1[k], o), n2 = __shfl_up(i2[k], o);
+                if (lane >= o) {
+                    i1[k] += n1;
+                    i2[k] += n2;
+                }
             }
         }
-        int run = ic - cs, nt = it - ts, nt2 = it2 - ts2;
+        // this lane's first tile of each class: the classes with more m-tiles come first
+        int p1[PLAN_NC], p2[PLAN_NC], t1 = 0, t2 = 0;
+#pragma unroll
+        for (int k = PLAN_NC - 1; k >= 0; --k) {
+            p1[k] = t1 + i1[k] - s1[k];
+            p2[k] = t2 + i2[k] - s2[k];
+            t1 += __shfl(i1[k], 63);
+            t2 += __shfl(i2[k], 63);
+        }
+        int run = ic - cs;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int e = 4 * lane + k;
             if (e < n_exp) {
                 tot[e] = run;
-                if (tiles)  // the group's tiles for the batched kernels: (expert, first position)
-                    for (int q = 0; q < t[k]; ++q) {
-                        tiles[1 + 2 * (nt + q)] = e;
-                        tiles[2 + 2 * (nt + q)] = run + q * cap;
-                    }
-                if (tiles2)
-                    for (int q = 0; q < t2[k]; ++q) {
-                        tiles2[1 + 2 * (nt2 + q)] = e;
-                        tiles2[2 + 2 * (nt2 + q)] = run + q * cap2;
-                    }
+                if (tiles) put_tiles(tiles, cap, e, c[k], run, p1);
+                if (tiles2) put_tiles(tiles2, cp2, e, c[k], run, p2);
             }
             run += c[k];
-            nt += t[k];
-            nt2 += t2[k];
         }
         if (lane == 63) {
             tot[n_exp] = ic;
-            if (tiles) tiles[0] = it;
-            if (tiles2) tiles2[0] = it2;
+            if (tiles) tiles[0] = t1;
+            if (tiles2) tiles2[0] = t2;
         }
     }
     __syncthreads();
