@@ -4,8 +4,8 @@
 //
 //   router (router.hip)   -> ids, weights, Q8_0 activation rows per token (K order of kperm)
 //   k_plan (router.hip)   -> pairs stably grouped by expert, each group cut into tiles of up to
-//                            32 pairs for gate/up and 48 for down (batches of 8+ pairs per expert
-//                            on average), or 4 (smaller)
+//                            48 pairs (batches of 8+ pairs per expert on average), or 4 (smaller),
+//                            listed with the tiles of the most m-tiles of 16 pairs first
 //   k_gateup_quad,        -> 4-pair tiles: one wave per (tile, 64 weight rows); the 16-block
 //   k_down_quad              v_mfma_i32_4x4x4_16b_i8 gives each lane its row's exact block sums
 //                            for the 4 pairs, so the f32 fold spends nothing on empty pair places
@@ -270,17 +270,16 @@ __device__ __forceinline__ int place_pair(int mt, int g, int i) { return 4 * (4 
 // Gate/up for one tile (blockIdx.y) of up to 16 MT pairs of expert e, TW row tiles per workgroup
 // (32 gate rows and the matching 32 up rows each, one RVM_PACK_GATE_UP tile), half a row tile per
 // wave: wave w takes row tile rt = TW blockIdx.x + w / 2, gate rows 16 h + m (piece h = w mod 2) and
-// the matching up rows (piece h + 2). Half-tile waves are twice as many, each half as long, at 110
-// VGPRs (four waves per SIMD, against three for whole row tiles at 168): the grid's last partial
-// round of workgroups leaves fewer SIMDs short of waves (512 tokens: 297 -> 275 us per call). A tile
-// of at most 16 pairs (the remainder of an expert's pairs after a full tile) runs the loop of its
-// one occupied m-tile: 16% fewer MFMAs, 11% fewer VALU instructions, the time within the run-to-run
-// spread (the second instance costs no wave).
+// the matching up rows (piece h + 2). Half-tile waves are twice as many, each half as long, at four
+// waves per SIMD (against three for whole row tiles): the grid's last partial round of workgroups
+// leaves fewer SIMDs short of waves (512 tokens: 297 -> 275 us per call). A tile runs the loop of
+// its occupied m-tiles only. Four waves per SIMD are asked for: 48-pair tiles need 145 VGPRs
+// otherwise (three waves); at 128 a few values outside the tile loop go to scratch.
 // h = gelu(gate) * up is quantised per pair to one Q8_0 block of 32 (runtime/src/ops.rs:95-105) and
 // stored in the K order of kperm; the block spans both waves' rows, so they exchange their maxima of
 // |h| in LDS (a maximum of non-negative values, the same bits in any order).
 template <int MT, int TW>
-__global__ __launch_bounds__(128 * TW) void k_gateup_mfma(const uint8_t *__restrict__ nib,
+__global__ __launch_bounds__(128 * TW) __attribute__((amdgpu_waves_per_eu(4))) void k_gateup_mfma(const uint8_t *__restrict__ nib,
                                                           const uint16_t *__restrict__ scl,
                                                           const int32_t *__restrict__ tiles,
                                                           const int32_t *__restrict__ gstart,
@@ -309,6 +308,8 @@ __global__ __launch_bounds__(128 * TW) void k_gateup_mfma(const uint8_t *__restr
     const size_t tb = ((size_t)e * Tg + (active ? rt : 0)) * nb;
     if (MT > 1 && cnt <= 16)  // a tile of at most 16 pairs runs the loop of its one occupied m-tile
         tile_sums<MT, 2, KC, 1, false, 2 * TW, 2>(nib, scl, tb, nb, active, xq8, xsc, d, n_tok, sh, acc, h);
+    else if (MT > 2 && cnt <= 32)
+        tile_sums<MT, 2, KC, (MT > 2 ? 2 : MT), false, 2 * TW, 2>(nib, scl, tb, nb, active, xq8, xsc, d, n_tok, sh, acc, h);
     else
         tile_sums<MT, 2, KC, MT, false, 2 * TW, 2>(nib, scl, tb, nb, active, xq8, xsc, d, n_tok, sh, acc, h);
     const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
@@ -654,17 +655,18 @@ int launch_experts_quad(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayou
 }
 
 // Pairs per tile: quads while the groups are small (fewer pairs than 8 per expert on average),
-// else the MFMA tiles (32 pairs for gate/up, 48 for down), so that a typical group fits one tile
+// else the MFMA tiles (48 pairs for gate/up and down), so that a typical group fits one tile
 // and its weights are streamed once.
 inline int tile_pairs(const rvm_layer *L, int n_tok) {
     const long pairs = (long)n_tok * L->top_k;
-    return pairs >= 8L * L->n_exp ? 32 : QUAD;
+    return pairs >= 8L * L->n_exp ? 48 : QUAD;
 }
 
 // The 16x16 MFMA kernels: gate/up on tiles of 16 MT pairs (lay.tiles), down on tiles of 16 MD pairs
-// (lay.tiles2). Gate/up keeps two m-tiles (with half row tiles per wave, three measured the same:
-// 276.5-277.9 against 277.8-278.9 us for 512 tokens); down runs three at three waves per SIMD (73
-// against 82.5 us), each of its tiles through the loop of only its occupied m-tiles.
+// (lay.tiles2). Both take three m-tiles: 48-pair tiles split fewer experts' pairs over two tiles,
+// whose weights are then streamed twice (gate/up 512 tokens: 241.5-243.6 against 244.6-246.3 us
+// with 32-pair tiles; down 73 against 82.5 us), each tile through the loop of only its occupied
+// m-tiles.
 template <int MT, int MD>
 int launch_experts(const rvm_layer *L, int n_tok, uint8_t *w, const WsLayout &lay) {
     const int32_t *tiles = (const int32_t *)(w + lay.tiles);
@@ -703,7 +705,7 @@ int moe_forward(const rvm_layer *L, const float *x, float *out, int n_tok, int f
     int32_t *pos_of = (int32_t *)(w + lay.pos_of);
     int rc = launch_router(L, x, n_tok, flags, xf, w, lay, ids, wts, nullptr, true);
     if (rc || (rc = span_router_done())) return rc;
-    constexpr int GU_MT = 2, DN_MT = 3;  // m-tiles per tile of the two MFMA kernels
+    constexpr int GU_MT = 3, DN_MT = 3;  // m-tiles per tile of the two MFMA kernels
     const int cap = tile_pairs(L, n_tok);
     const bool quad = cap == QUAD;
     if ((rc = launch_plan(ids, n_tok * L->top_k, L->n_exp, (int32_t *)(w + lay.order), pos_of,
