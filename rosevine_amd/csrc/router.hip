@@ -491,38 +491,74 @@ __device__ __forceinline__ void plan_load(const int32_t *__restrict__ ids, int b
         ev[r] = i < hi ? ids[i] : -1;
     }
 }
+// Inclusive prefix sum of an int over the 64 lanes (all active), by DPP only: row_shr 1, 2, 4, 8
+// within each row of 16 (lanes whose source lies outside the row add 0), then row_bcast:15 (row
+// r's last lane into row r + 1, for rows 1 and 3) and row_bcast:31 (lane 31 into rows 2 and 3).
+__device__ __forceinline__ int wave_scan_i(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, true);
+    return v;
+}
+
 // Tile classes: a tile of n pairs has class min(PLAN_NC, ceil(n / 16)) - 1 (its m-tiles of 16 pairs).
 // The tiles are listed class by class, the most m-tiles first, and by expert within a class: the
 // batched kernels' workgroups start in grid order, so the longest tiles start first and the
 // remainder tiles, which run fewer m-tiles, fill the end of the grid.
 constexpr int PLAN_NC = 3;
 __device__ __forceinline__ int tile_class(int n) { return min(PLAN_NC, (n + 15) / 16) - 1; }
-// Adds the tiles of a group of n pairs (tiles of up to cap) to the per-class counts.
-__device__ __forceinline__ void tile_counts(int n, int cap, int (&cnt)[PLAN_NC]) {
-    const int full = n / cap, rem = n - full * cap;
-    const int kf = tile_class(cap), kr = rem ? tile_class(rem) : -1;
-#pragma unroll
-    for (int k = 0; k < PLAN_NC; ++k) cnt[k] += (k == kf ? full : 0) + (k == kr ? 1 : 0);
+// n / cap for 0 <= n < 2^20 and 1 <= cap <= 128 (inv = 1 / cap as f32): the f32 estimate is within
+// one of the quotient and is corrected once each way (checked for every such n and cap).
+__device__ __forceinline__ int div_small(int n, int cap, float inv) {
+    int q = (int)((float)n * inv);
+    q += (q + 1) * cap <= n ? 1 : 0;
+    q -= q * cap > n ? 1 : 0;
+    return q;
 }
-// Writes the tiles (expert, first position in order) of expert e's group of n pairs at run: full
-// tiles of cap pairs, then the remainder, each at the next place of its class (pos).
-__device__ __forceinline__ void put_tiles(int32_t *__restrict__ tl, int cap, int e, int n, int run,
-                                          int (&pos)[PLAN_NC]) {
-    const int full = n / cap, rem = n - full * cap;
-    const int kf = tile_class(cap), kr = rem ? tile_class(rem) : -1;
+// A group of n pairs in tiles of up to cap: full tiles of cap pairs (class kf, wave-uniform), then
+// the remainder's tile (class kr, -1 when there is none).
+struct GroupTiles {
+    int full, kr;
+};
+__device__ __forceinline__ GroupTiles group_tiles(int n, int cap, float inv) {
+    const int full = div_small(n, cap, inv), rem = n - full * cap;
+    return GroupTiles{full, rem ? tile_class(rem) : -1};
+}
+// Adds a group's tiles to the per-class counts.
+__device__ __forceinline__ void tile_counts(const GroupTiles &t, int kf, int (&cnt)[PLAN_NC]) {
+#pragma unroll
+    for (int k = 0; k < PLAN_NC; ++k) cnt[k] += (k == kf ? t.full : 0) + (k == t.kr ? 1 : 0);
+}
+// The places of a group's tiles in the list: its full tiles from *f on, its remainder's at *r (-1
+// when there is none); pos holds the next place of each class.
+__device__ __forceinline__ void place_tiles(const GroupTiles &t, int kf, int (&pos)[PLAN_NC], int *f, int *r) {
+    int fp = 0, rp = -1;
 #pragma unroll
     for (int k = 0; k < PLAN_NC; ++k) {
-        if (k == kf)
-            for (int q = 0; q < full; ++q) {
-                tl[1 + 2 * pos[k]] = e;
-                tl[2 + 2 * pos[k]] = run + q * cap;
-                ++pos[k];
-            }
-        if (k == kr) {
-            tl[1 + 2 * pos[k]] = e;
-            tl[2 + 2 * pos[k]] = run + full * cap;
-            ++pos[k];
+        if (k == kf) {
+            fp = pos[k];
+            pos[k] += t.full;
         }
+        if (k == t.kr) rp = pos[k]++;
+    }
+    *f = fp;
+    *r = rp;
+}
+// Writes expert e's tiles (expert, first position in order) for its n pairs at run, at the places
+// place_tiles gave.
+__device__ __forceinline__ void put_tiles(int32_t *__restrict__ tl, int cap, float inv, int e, int n, int run,
+                                          int f, int r) {
+    const int full = div_small(n, cap, inv);
+    for (int q = 0; q < full; ++q) {
+        tl[1 + 2 * (f + q)] = e;
+        tl[2 + 2 * (f + q)] = run + q * cap;
+    }
+    if (r >= 0) {
+        tl[1 + 2 * r] = e;
+        tl[2 + 2 * r] = run + full * cap;
     }
 }
 
@@ -532,6 +568,7 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
                                                int32_t *__restrict__ tiles2, int cap2) {
     __shared__ int cnt[16][256];
     __shared__ int tot[257];
+    __shared__ int tplace[2][2][256];  // per tile list and expert: first full tile's place, remainder's
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int chunk = ((n + 15) / 16 + 63) / 64 * 64;
     const int lo = w * chunk, hi = min(n, lo + chunk);
@@ -555,7 +592,10 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
     __syncthreads();
     if (w == 0) {  // exclusive scans of the group sizes and of their tile counts by class, 4 experts a lane
         const int cp2 = tiles2 ? cap2 : 1;
+        const float inv1 = 1.0f / (float)cap, inv2 = 1.0f / (float)cp2;
+        const int kf1 = tile_class(cap), kf2 = tile_class(cp2);
         int c[4], cs = 0, s1[PLAN_NC], s2[PLAN_NC];
+        GroupTiles g1[4], g2[4];
 #pragma unroll
         for (int k = 0; k < PLAN_NC; ++k) s1[k] = s2[k] = 0;
 #pragma unroll
@@ -563,27 +603,17 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
             const int e = 4 * lane + k;
             c[k] = e < n_exp ? tot[e] : 0;
             cs += c[k];
-            tile_counts(c[k], cap, s1);
-            tile_counts(c[k], cp2, s2);
+            g1[k] = group_tiles(c[k], cap, inv1);
+            g2[k] = group_tiles(c[k], cp2, inv2);
+            tile_counts(g1[k], kf1, s1);
+            tile_counts(g2[k], kf2, s2);
         }
-        int ic = cs, i1[PLAN_NC], i2[PLAN_NC];
+        const int ic = wave_scan_i(cs);
+        int i1[PLAN_NC], i2[PLAN_NC];
 #pragma unroll
         for (int k = 0; k < PLAN_NC; ++k) {
-            i1[k] = s1[k];
-            i2[k] = s2[k];
-        }
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int nc = __shfl_up(ic, o);
-            if (lane >= o) ic += nc;
-#pragma unroll
-            for (int k = 0; k < PLAN_NC; ++k) {
-                const int n1 = __shfl_up(i1[k], o), n2 = __shfl_up(i2[k], o);
-                if (lane >= o) {
-                    i1[k] += n1;
-                    i2[k] += n2;
-                }
-            }
+            i1[k] = wave_scan_i(s1[k]);
+            i2[k] = wave_scan_i(s2[k]);
         }
         // this lane's first tile of each class: the classes with more m-tiles come first
         int p1[PLAN_NC], p2[PLAN_NC], t1 = 0, t2 = 0;
@@ -591,8 +621,8 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
         for (int k = PLAN_NC - 1; k >= 0; --k) {
             p1[k] = t1 + i1[k] - s1[k];
             p2[k] = t2 + i2[k] - s2[k];
-            t1 += __shfl(i1[k], 63);
-            t2 += __shfl(i2[k], 63);
+            t1 += __builtin_amdgcn_readlane(i1[k], 63);
+            t2 += __builtin_amdgcn_readlane(i2[k], 63);
         }
         int run = ic - cs;
 #pragma unroll
@@ -600,8 +630,8 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
             const int e = 4 * lane + k;
             if (e < n_exp) {
                 tot[e] = run;
-                if (tiles) put_tiles(tiles, cap, e, c[k], run, p1);
-                if (tiles2) put_tiles(tiles2, cp2, e, c[k], run, p2);
+                place_tiles(g1[k], kf1, p1, &tplace[0][0][e], &tplace[0][1][e]);
+                place_tiles(g2[k], kf2, p2, &tplace[1][0][e], &tplace[1][1][e]);
             }
             run += c[k];
         }
@@ -613,7 +643,11 @@ __global__ __launch_bounds__(1024) void k_plan(const int32_t *__restrict__ ids, 
     }
     __syncthreads();
     if ((int)threadIdx.x <= n_exp) gstart[threadIdx.x] = tot[threadIdx.x];
-    if ((int)threadIdx.x < n_exp) {
+    if ((int)threadIdx.x < n_exp) {  // one expert a thread: its tiles, then its waves' first positions
+        const int e = threadIdx.x, ne = tot[e + 1] - tot[e];
+        if (tiles) put_tiles(tiles, cap, 1.0f / (float)cap, e, ne, tot[e], tplace[0][0][e], tplace[0][1][e]);
+        if (tiles2)
+            put_tiles(tiles2, cap2, 1.0f / (float)cap2, e, ne, tot[e], tplace[1][0][e], tplace[1][1][e]);
         int run = tot[threadIdx.x];
         for (int ww = 0; ww < 16; ++ww) {
             const int c = cnt[ww][threadIdx.x];
@@ -698,6 +732,8 @@ int launch_router(const rvm_layer *L, const float *x, int n_tok, int flags, cons
 int launch_plan(const int32_t *ids, int n_pairs, int n_exp, int32_t *order, int32_t *pos_of, int32_t *gstart,
                 int32_t *tiles, int cap, int32_t *tiles2, int cap2) {
     RVM_CHECK(cap >= 1 && (!tiles2 || cap2 >= 1));
+    // the tile counts' division (div_small) holds for groups below 2^20 pairs and tiles of <= 128
+    RVM_CHECK(!tiles || (n_pairs < (1 << 20) && cap <= 128 && (!tiles2 || cap2 <= 128)));
     hipLaunchKernelGGL(k_plan, dim3(1), dim3(1024), 0, cur_stream(), ids, n_pairs, n_exp, order, pos_of, gstart,
                        tiles, cap, tiles2, cap2);
     return launched();
