@@ -497,22 +497,25 @@ __device__ __forceinline__ void stage_quad_rows(const int8_t *__restrict__ src, 
 }
 
 // The four pairs' sequential folds of this lane's weight row over blocks 0 .. nb-1 (a multiple of
-// QD). entry(b): the lane's 16-byte weight entry of block b (its scale has the same index in scl);
-// stage(): fills lds, the wave's staged rows (the lane's pair is lane & 3). The weight loads run QD
-// blocks ahead in a ring of registers.
-template <int QD, class Entry, class Stage>
+// QD). The lane's 16-byte weight entry of block b is entry lane_entry + boff(b) of the planes from
+// nib and scl (its scale has the same index; entries: the planes' extent there, in entries), with
+// boff(b) wave-uniform: the loads go through buffer descriptors with boff in a scalar register, so
+// they cost no vector address arithmetic. stage(): fills lds, the wave's staged rows (the lane's
+// pair is lane & 3). The weight loads run QD blocks ahead in a ring of registers.
+template <int QD, class BlockOff, class Stage>
 __device__ __forceinline__ void quad_row_sums(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl,
-                                              Entry entry, Stage stage, const uint8_t *lds, int width,
-                                              float (&acc)[4]) {
+                                              uint32_t entries, uint32_t lane_entry, BlockOff boff, Stage stage,
+                                              const uint8_t *lds, int width, float (&acc)[4]) {
     const int nb = width / QK, i = threadIdx.x & 3;
     const uint8_t *xl = lds + i * quad_pitch(width);
     const float4 *sl = (const float4 *)(lds + 4 * quad_pitch(width));
+    const __amdgpu_buffer_rsrc_t wres = buffer_rsrc(nib, entries * 16u), sres = buffer_rsrc(scl, entries * 2u);
     uint4 w[QD];
     uint32_t s[QD];
     auto load = [&](int u, int b) {
-        const size_t e = entry(b);
-        w[u] = nib[e];
-        s[u] = scl[e];
+        const uint32_t so = (uint32_t)boff(b);
+        w[u] = buffer_load_u4(wres, lane_entry * 16u, so * 16u);
+        s[u] = buffer_load_u16(sres, lane_entry * 2u, so * 2u);
     };
     auto compute = [&](int u, int b) {
         const uint4 x0 = *(const uint4 *)(xl + 32 * b), x1 = *(const uint4 *)(xl + 32 * b + 16);
@@ -563,10 +566,10 @@ __global__ __launch_bounds__(64) void k_gateup_quad(const uint4 *__restrict__ ni
     uint8_t *lds = (uint8_t *)quad_lds;
     // the rows of the quad's pairs; a missing pair takes pair 0's row and is not stored
     const int tok = lane < 4 ? order[k0 + (lane < cnt ? lane : 0)] / top_k : 0;
-    const size_t tb = ((size_t)e * Tg + rt) * nb;
+    const size_t tb = ((size_t)e * Tg + rt) * nb;  // the row tile's first entry group
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     quad_row_sums<QD>(
-        nib, scl, [&](int b) { return (tb + (size_t)b) * 64 + lane; },
+        nib + tb * 64, scl + tb * 64, (uint32_t)nb * 64u, (uint32_t)lane, [&](int b) { return b * 64; },
         [&]() { stage_quad_rows(xq8, xsc, tok, d, lds); }, lds, d, acc);
     float o[4];
 #pragma unroll
@@ -603,14 +606,14 @@ __global__ __launch_bounds__(64) void k_down_quad(const uint4 *__restrict__ nib,
     const int lane = threadIdx.x, S = ff / 64, Td = d / 32;
     if ((int)blockIdx.x >= d / 64) return;  // the padding of the grid's rows
     uint8_t *lds = (uint8_t *)quad_lds;
-    const size_t tb = ((size_t)e * Td + 2 * blockIdx.x + (lane >> 5)) * S;
+    const size_t tb = ((size_t)e * Td + 2 * blockIdx.x) * S;  // the two row tiles' first entry group
     const int place = lane & 31;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     quad_row_sums<QD>(
-        nib, scl,
+        nib + tb * 64, scl + tb * 64, 2u * (uint32_t)S * 64u, (uint32_t)((lane >> 5) * S * 64 + place),
         [&](int b) {
             const int half = b >= S ? 1 : 0;
-            return (tb + (size_t)(b - half * S)) * 64 + 32 * half + place;
+            return (b - half * S) * 64 + 32 * half;
         },
         [&]() { stage_quad_rows(hq8, hsc, k0 + (lane < cnt ? lane : 0), ff, lds); }, lds, ff, acc);
     const int row = 64 * blockIdx.x + lane;
