@@ -30,30 +30,40 @@ constexpr int SEL_WAVES = 8;  // waves of the selecting workgroup
 
 // The logit statistics of one router row and one token: S = the f64 sum of the f32 products
 // (lane chunks summed in order, then a DPP wave scan), and the bound on the sequential f32 fold's
-// error from the prefix sums. Every lane returns the same pair.
+// error, g sum_i |s_i| / (1 - d g) with g = u / (1 - u), from a bound on the sum of the exact
+// prefix sums' magnitudes. A lane with the C elements a .. a + C - 1 bounds its share from f32
+// prefixes: q_0 = fl(r), r the f64 sum of the lanes below, and q_k = fl(q_(k-1) + p_(a+k-1)).
+// Each rounding moves a prefix by at most g |q_k| (u |r| for q_0), so |s_(a+k-1)| <= |q_k| + u |r|
+// + g (|q_1| + ... + |q_k|), and the lane's share is at most Q (1 + C g)^2 + C u |r|, with Q the
+// f32 sum of the |q_k| in order (at most (1 + C g) times smaller than their exact sum); C g is
+// about 2^-18 at most (C <= 64), so Q (1 + 2^-16) covers the factor. The f32 chains cost half
+// what f64 ones do.
+// Every lane returns the same pair.
 template <int F4>
 __device__ __forceinline__ double2 row_stats(const float4 (&wv)[F4], const float4 (&xv)[F4], int lane) {
     constexpr int d = 256 * F4, C = 4 * F4;
-    double p[C];  // the f32 products, exactly, as f64
+    static_assert(C <= 64, "the lane share's factor (1 + C g)^2 is covered by 1 + 2^-16");
+    float pf[C];  // the f32 products
 #pragma unroll
     for (int i = 0; i < F4; ++i) {
-        p[4 * i] = (double)(wv[i].x * xv[i].x);
-        p[4 * i + 1] = (double)(wv[i].y * xv[i].y);
-        p[4 * i + 2] = (double)(wv[i].z * xv[i].z);
-        p[4 * i + 3] = (double)(wv[i].w * xv[i].w);
+        pf[4 * i] = wv[i].x * xv[i].x;
+        pf[4 * i + 1] = wv[i].y * xv[i].y;
+        pf[4 * i + 2] = wv[i].z * xv[i].z;
+        pf[4 * i + 3] = wv[i].w * xv[i].w;
     }
     double c = 0.0;
 #pragma unroll
-    for (int i = 0; i < C; ++i) c += p[i];
+    for (int i = 0; i < C; ++i) c += (double)pf[i];
     const double incl = wave_scan_d(c);
-    double run = dpp_zero_d<0x138>(incl);  // wave_shr:1: the sum of the lanes below
+    const double run = dpp_zero_d<0x138>(incl);  // wave_shr:1: the sum of the lanes below
     const double total = readlane_d(incl, 63);
-    double babs = 0.0;
+    float q = (float)run, qs = 0.0f;
 #pragma unroll
     for (int i = 0; i < C; ++i) {
-        run += p[i];
-        babs += fabs(run);
+        q = q + pf[i];
+        qs = qs + fabsf(q);
     }
+    double babs = (double)qs * (1.0 + 0x1p-16) + (double)C * 0x1p-24 * fabs(run);
     babs = wave_sum_d(babs);
     const double u = 0x1p-24, g = u / (1.0 - u);
     return make_double2(total, babs * g / (1.0 - (double)d * g) * (1.0 + 0x1p-20) + 1e-300);
@@ -143,30 +153,37 @@ __global__ __launch_bounds__(BW * 64) void k_router_batch(const float *__restric
     for (int i = 0; i < F4; ++i) wv[i] = w4[i];
     const int t0 = blockIdx.y * RT, t1 = min(t0 + RT, n_tok);
     const int base0 = (blockIdx.x * BW + w) * 2, step = gridDim.x * BW * 2;
+    // this lane's element of the first Q8_0 block it quantises (block hb0), loaded a token ahead
+    // with the token's chunk
+    const int hb0 = base0 + (lane >> 5), qoff = min(hb0, nb - 1) * QK + (lane & 31);
     float4 xr[F4];
+    float qr;
     {
         const float4 *x4 = (const float4 *)(x + (size_t)t0 * d) + lane * F4;
 #pragma unroll
         for (int i = 0; i < F4; ++i) xr[i] = x4[i];
+        qr = x[(size_t)t0 * d + qoff];
     }
     for (int t = t0; t < t1; ++t) {
         const float *xt = x + (size_t)t * d;
         float4 xv[F4];
 #pragma unroll
         for (int i = 0; i < F4; ++i) xv[i] = xr[i];
+        const float qv = qr;
         {  // the next token's chunk (the last one again at the end; unused)
-            const float4 *x4 = (const float4 *)(x + (size_t)min(t + 1, t1 - 1) * d) + lane * F4;
+            const size_t tn = (size_t)min(t + 1, t1 - 1) * d;
+            const float4 *x4 = (const float4 *)(x + tn) + lane * F4;
 #pragma unroll
             for (int i = 0; i < F4; ++i) xr[i] = x4[i];
+            qr = x[tn + qoff];
         }
         float scale = 1.0f;
         if (xf.pre_norm) {
             scale = norm_x_chunk<F4>(xt, xv, xf.eps);
             router_gain<F4>(xf, lane, xv);
         }
-        const int hb0 = base0 + (lane >> 5);
-        quant_x_blocks<F4>(xt, xf, scale, base0, step, hb0 < nb ? xt[hb0 * QK + (lane & 31)] : 0.0f, nullptr,
-                           xq8 + (size_t)t * d, xsc + (size_t)t * nb, lane);
+        quant_x_blocks<F4>(xt, xf, scale, base0, step, hb0 < nb ? qv : 0.0f, nullptr, xq8 + (size_t)t * d,
+                           xsc + (size_t)t * nb, lane);
         if (have) {
             const double2 st = row_stats<F4>(wv, xv, lane);
             if (lane == 0) stats[(size_t)t * n_exp + e] = st;
