@@ -269,6 +269,7 @@ __device__ __forceinline__ float load_x_chunk(const float *xt, int lane, const X
     return s;
 }
 
+constexpr int SEL_P_FLOATS = 2 * 16 * 260;  // >= 128 * 36
 // LDS of select_token for a workgroup of NW waves and d = 256 * F4.
 template <int F4, int NW>
 struct SelShared {
@@ -285,7 +286,8 @@ struct SelShared {
     int badw[NW];
     int pass;
     alignas(16) float xs[256 * F4];  // the exact path's layer input (x, or rms_norm(x))
-    alignas(16) float P[128 * 36];   // the exact path's products: 128 rows x 32 columns, pitch 36
+    alignas(16) float P[SEL_P_FLOATS];  // the exact paths' products: 128 rows x 32 columns at pitch
+                                        // 36 (exact_all), or two buffers of 16 rows x 256 at 260
     int cand[32];                    // the candidate path's experts, ascending
     float csp[32], csel[9];          // their softmax numerators; ranks 0 .. 8 in order
     int ncand, cok;
@@ -372,8 +374,8 @@ __device__ void exact_all(SelShared<F4, NW> &sh, const float *__restrict__ W, co
 template <int F4, int NW>
 __device__ bool exact_candidates(SelShared<F4, NW> &sh, const float *__restrict__ W, const float *__restrict__ bias,
                                  const float *__restrict__ xt, int n_exp, int top_k, const XForm &xf) {
-    constexpr int d = 256 * F4, CM = 16, CK = 128, NCH = d / CK, PP = CK + 4, D = 6;
-    static_assert(2 * CM * PP <= 128 * 36, "two product buffers fit the exact path's LDS");
+    constexpr int d = 256 * F4, CM = 16, CK = 256, NCH = d / CK, PP = CK + 4, D = 3;
+    static_assert(2 * CM * PP <= SEL_P_FLOATS, "two product buffers fit the exact path's LDS");
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -521,19 +523,23 @@ __device__ bool exact_candidates(SelShared<F4, NW> &sh, const float *__restrict_
         ok = __ballot(!ok) == 0;
         if (lane < nc && rk < top_k) sh.sel[rk] = ce;
         // weights (tolerance class, as on the certified path): the candidates' exact numerators,
-        // the others' from the estimates, an f64 sum in index order, renormalised over the top k
+        // the others' from the estimates, their f64 sum, renormalised over the top k
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = lane + 64 * i;
-            if (e < n_exp) sh.sp[e] = (float)exp((double)((float)sh.Sx[e] - Mf));
+            if (e < n_exp) sh.sp[e] = expf((float)sh.Sx[e] - Mf);
         }
         wave_lds_sync();
         if (lane < nc) sh.sp[ce] = spc;
         wave_lds_sync();
-        double sum = 0.0;
-        if (lane == 0)
-            for (int j = 0; j < n_exp; ++j) sum += (double)sh.sp[j];
-        const float inv = (float)(1.0 / __shfl(sum, 0));
+        double sum = 0.0;  // a tree over the wave, as on the certified path (the weights' class)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = lane + 64 * i;
+            if (e < n_exp) sum += (double)sh.sp[e];
+        }
+        sum = wave_sum_d(sum);
+        const float inv = (float)(1.0 / sum);
         if (ok && lane < top_k) {
             float s = -0.0f;
             for (int j = 0; j < top_k; ++j) s = s + sh.csel[j] * inv;
