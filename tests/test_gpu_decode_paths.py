@@ -10,7 +10,8 @@ the CPU (tests/routing_cases.py) force each outcome for one token:
 - the same experts in another slot order (moved h rows);
 - tied f32 keys, so that every workgroup computes experts 0..k-1 and the selected experts come
   from correction rows (the full exact path: the output is the oracle's bits);
-- RVM_EXACT_SELECT on every token.
+- RVM_EXACT_SELECT on every token (also at widths of one, two and four 256-column chunks of the
+  candidates' folds).
 
 Each case asserts that a fallback was taken, that the ids are the oracle's, and that the output
 agrees with the oracle (the layer tolerance, and bitwise where the full exact path ran).
@@ -171,3 +172,35 @@ def test_stack30_decode_teacher_forced(gpu, orc):
         hip.Stream.use_default()
         hip.sync()
         s.close()
+
+
+@pytest.mark.parametrize("d,ff", [(256, 64), (512, 128), (1024, 128)])
+def test_decode_exact_select_small_widths(gpu, orc, d, ff):
+    """RVM_EXACT_SELECT through decode at widths of one, two and four 256-column chunks of the
+    candidates' exact folds (the ring of chunk loads runs past the row's end and reloads its last
+    chunk, unused): ids and weights are the oracle's, outputs within the layer tolerance."""
+    n_exp, top_k, n = 16, 4, 6
+    rng = np.random.default_rng([SEED, d, 91])
+    gate_up = hip.synth_q4_host(n_exp, 2 * ff, d, SEED, 3000 + d)
+    down = hip.synth_q4_host(n_exp, d, ff, SEED, 4000 + d)
+    router = synth.router_weights(SEED, 5, n_exp, d)
+    dscale = rng.uniform(0.5, 1.5, n_exp).astype(np.float32)
+    L = moe.MoeLayer(n_exp, top_k, d, ff, router, None, dscale)
+    L.load_q4(gate_up, down)
+    x = synth.tokens(SEED + 23 + d, n, d=d)
+    ws = moe.Workspace(L, 1)
+    xd, out = dev(x), DevBuf(n * d * 4)
+    ids_ref, w_ref, _ = orc.select_experts(orc.router_logits(router, None, x, n_exp, d), top_k)
+    for t in range(n):
+        moe.decode(L, xd, out, ws, flags=hip.EXACT_SELECT, x_off=t * d * 4, out_off=t * d * 4)
+        ids, w = ws.selection(L, 1)
+        assert np.array_equal(ids[0], ids_ref[t].astype(np.int32)), (d, t)
+        assert np.max(np.abs(w[0] - w_ref[t])) <= 1e-6, (d, t)
+    assert ws.fallbacks() == n
+    got = out.download(np.float32, n * d).reshape(n, d)
+    rows = lambda raw, n_out, k: raw.reshape(n_exp, n_out * (k // 32) * 18)
+    gu = {e: rows(gate_up, 2 * ff, d)[e] for e in range(n_exp)}
+    dn = {e: rows(down, d, ff)[e] for e in range(n_exp)}
+    want = orc.experts_q8(gu, dn, dscale, x, d, ff, ids_ref, w_ref, n_exp)
+    for t in range(n):
+        assert_close(got[t], want[t], f"d {d} token {t}")
