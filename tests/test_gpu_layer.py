@@ -7,8 +7,9 @@ tests also hold them to 2e-5 of the RMS, which any quantisation flip would excee
 Workloads are the seeded synthetic configurations at the reference's shapes (128 experts, top-8,
 d = 2816, ff = 704): single-token decode, a ragged 32-token decode batch with Zipf(1.1)
 popularity, a 512-token prefill, and a teacher-forced multi-layer stack with router bias and
-an RMSNorm between layers. Size-independent properties (batch invariance, graph replays) cover
-what the oracle is too slow to check in full.
+an RMSNorm between layers; and 16-expert layers of other widths through each batched path.
+Size-independent properties (batch invariance, graph replays) cover what the oracle is too slow
+to check in full.
 """
 import numpy as np
 import pytest
@@ -335,3 +336,38 @@ def test_stack_teacher_forced(gpu, orc):
             assert_close(got[t], out_ref[t], f"layer {layer} token {t}")
         cur = got
 
+
+
+@pytest.mark.parametrize("d,ff", [(512, 128), (1024, 256)])
+@pytest.mark.parametrize("n", [8, 64, 300])
+def test_forward_small_shapes_match_oracle(gpu, orc, d, ff, n):
+    """rvm_moe_forward at shapes other than the reference's, through each batched path: 8 tokens of
+    16 experts at top-4 take the 4-pair tiles, 64 the 16x16 MFMA tiles after the certified
+    selection, 300 the MFMA tiles after the exact logits (the tile loops' whole chunks at other
+    block counts, the down rows' two halves at other widths). Ids are the oracle's; outputs agree
+    with the oracle, bit for bit on the exact-logit path."""
+    n_exp, top_k = 16, 4
+    rng = np.random.default_rng([SEED, d, ff, 93])
+    gate_up = hip.synth_q4_host(n_exp, 2 * ff, d, SEED, 5000 + d + ff)
+    down = hip.synth_q4_host(n_exp, d, ff, SEED, 6000 + d + ff)
+    router = synth.router_weights(SEED, 7, n_exp, d)
+    dscale = rng.uniform(0.5, 1.5, n_exp).astype(np.float32)
+    L = moe.MoeLayer(n_exp, top_k, d, ff, router, None, dscale)
+    L.load_q4(gate_up, down)
+    x = synth.tokens(SEED + 31 + n, n, d=d)
+    ws = moe.Workspace(L, n)
+    xd, out = dev(x), DevBuf(n * d * 4)
+    moe.forward(L, xd, out, n, ws)
+    got = out.download(np.float32, n * d).reshape(n, d)
+    ids, w = ws.selection(L, n)
+    want_ids, want_w, _ = orc.select_experts(orc.router_logits(router, None, x, n_exp, d), top_k)
+    assert np.array_equal(ids, want_ids.astype(np.int32))
+    rows = lambda raw, n_out, k: raw.reshape(n_exp, n_out * (k // 32) * 18)
+    gu = {e: rows(gate_up, 2 * ff, d)[e] for e in range(n_exp)}
+    dn = {e: rows(down, d, ff)[e] for e in range(n_exp)}
+    want = orc.experts_q8(gu, dn, dscale, x, d, ff, want_ids, want_w, n_exp)
+    for t in range(n):
+        assert_close(got[t], want[t], f"d {d} ff {ff} n {n} token {t}")
+    if n >= 256:
+        assert np.array_equal(w, want_w)
+        assert np.array_equal(got, want.astype(np.float32)), "not the oracle's bits"
