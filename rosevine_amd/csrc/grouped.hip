@@ -291,6 +291,7 @@ __global__ __launch_bounds__(128 * TW) __attribute__((amdgpu_waves_per_eu(4))) v
     constexpr int R = 16 * MT, KC = GU_KC;
     __shared__ TileLds<MT, 2, KC, 2 * TW> sh;
     __shared__ float hmax[2 * TW][MT][4][4];  // [wave][m-tile][i][g]: max of |h| over the wave's 16 rows
+    __shared__ alignas(8) float qsc[TW][R][2];  // [row tile][tile place]: the Q8_0 block's d and 1/d
     const int tile = blockIdx.y;
     if (tile >= tiles[0]) return;
     const int e = tiles[1 + 2 * tile], k0 = tiles[2 + 2 * tile];
@@ -325,21 +326,31 @@ __global__ __launch_bounds__(128 * TW) __attribute__((amdgpu_waves_per_eu(4))) v
         }
     }
     __syncthreads();
+    // each block's scale d = amax / 127 and 1/d once, by one thread per (row tile, tile place),
+    // instead of in every lane of the block's 16 rows in both waves (places without a pair
+    // compute from maxima that were not written: unused)
+    if ((int)threadIdx.x < TW * R) {
+        const int rtl = threadIdx.x / R, p = threadIdx.x - rtl * R;
+        const int pm = p >> 4, pg = (p >> 2) & 3, pi = p & 3;
+        const float amax = fmaxf(hmax[2 * rtl][pm][pi][pg], hmax[2 * rtl + 1][pm][pi][pg]);
+        const float dq = amax / 127.0f;
+        qsc[rtl][p][0] = dq;
+        qsc[rtl][p][1] = dq != 0.0f ? 1.0f / dq : 0.0f;
+    }
+    __syncthreads();
     if (!active) return;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             if (place_pair(mt, 0, i) >= cnt) break;
-            const float amax = fmaxf(hmax[wv & ~1][mt][i][g], hmax[wv | 1][mt][i][g]);
-            const float dq = amax / 127.0f;
-            const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
-            const int q = sat_i8(roundf(hv[mt][i] * id));
+            const float2 dqi = *(const float2 *)qsc[wv >> 1][16 * mt + 4 * g + i];
+            const int q = sat_i8(roundf(hv[mt][i] * dqi.y));
             const int pr = place_pair(mt, g, i);
             if (pr < cnt) {
                 int8_t *hrow = hq8 + (size_t)(k0 + pr) * ff + rt * QK;
                 hrow[kperm(16 * h + m)] = (int8_t)q;
-                if (h == 0 && m == 0) hsc[(size_t)(k0 + pr) * Tg + rt] = h2f(f2h_rne(dq));
+                if (h == 0 && m == 0) hsc[(size_t)(k0 + pr) * Tg + rt] = h2f(f2h_rne(dqi.x));
             }
         }
     }
