@@ -472,11 +472,12 @@ __device__ __forceinline__ v4i quad_sums16(uint4 w, uint4 x0, uint4 x1) {
 
 // acc[i] = acc[i] + (16 sumi_i as f32) * (d_w / 16 * d_x_i), the reference's term (dw holds d_w / 16,
 // dx the four pairs' d_x: d_w * d_x is exact in f32 for binary16 scales, and so is its sixteenth).
+// Only the first NP pairs are folded (the MFMA forms all four sums either way).
+template <int NP>
 __device__ __forceinline__ void quad_fold(float (&acc)[4], v4i s16, float dw, float4 dx) {
-    acc[0] = acc[0] + (float)s16[0] * (dw * dx.x);
-    acc[1] = acc[1] + (float)s16[1] * (dw * dx.y);
-    acc[2] = acc[2] + (float)s16[2] * (dw * dx.z);
-    acc[3] = acc[3] + (float)s16[3] * (dw * dx.w);
+    const float dxi[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+    for (int i = 0; i < NP; ++i) acc[i] = acc[i] + (float)s16[i] * (dw * dxi[i]);
 }
 
 // The wave's LDS region: the four pairs' activation rows (K order of kperm) at a pitch of
@@ -513,7 +514,7 @@ __device__ __forceinline__ void stage_quad_rows(const int8_t *__restrict__ src, 
 // boff(b) wave-uniform: the loads go through buffer descriptors with boff in a scalar register, so
 // they cost no vector address arithmetic. stage(): fills lds, the wave's staged rows (the lane's
 // pair is lane & 3). The weight loads run QD blocks ahead in a ring of registers.
-template <int QD, class BlockOff, class Stage>
+template <int QD, int NP, class BlockOff, class Stage>
 __device__ __forceinline__ void quad_row_sums(const uint4 *__restrict__ nib, const uint16_t *__restrict__ scl,
                                               uint32_t entries, uint32_t lane_entry, BlockOff boff, Stage stage,
                                               const uint8_t *lds, int width, float (&acc)[4]) {
@@ -530,7 +531,7 @@ __device__ __forceinline__ void quad_row_sums(const uint4 *__restrict__ nib, con
     };
     auto compute = [&](int u, int b) {
         const uint4 x0 = *(const uint4 *)(xl + 32 * b), x1 = *(const uint4 *)(xl + 32 * b + 16);
-        quad_fold(acc, quad_sums16(w[u], x0, x1), h2f((uint16_t)s[u]) * 0.0625f, sl[b]);
+        quad_fold<NP>(acc, quad_sums16(w[u], x0, x1), h2f((uint16_t)s[u]) * 0.0625f, sl[b]);
     };
     // The first round only loads (and then stages the activation rows, their loads behind the
     // weights'): it is the same code as the later rounds, so the loads are issued in the same order
@@ -579,9 +580,13 @@ __global__ __launch_bounds__(64) void k_gateup_quad(const uint4 *__restrict__ ni
     const int tok = lane < 4 ? order[k0 + (lane < cnt ? lane : 0)] / top_k : 0;
     const size_t tb = ((size_t)e * Tg + rt) * nb;  // the row tile's first entry group
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    quad_row_sums<QD>(
-        nib + tb * 64, scl + tb * 64, (uint32_t)nb * 64u, (uint32_t)lane, [&](int b) { return b * 64; },
-        [&]() { stage_quad_rows(xq8, xsc, tok, d, lds); }, lds, d, acc);
+    auto rows = [&](auto np) {
+        quad_row_sums<QD, decltype(np)::value>(
+            nib + tb * 64, scl + tb * 64, (uint32_t)nb * 64u, (uint32_t)lane, [&](int b) { return b * 64; },
+            [&]() { stage_quad_rows(xq8, xsc, tok, d, lds); }, lds, d, acc);
+    };
+    if (cnt <= 2) rows(std::integral_constant<int, 2>{});  // a tile of one or two pairs folds two
+    else rows(std::integral_constant<int, 4>{});
     float o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = __shfl_xor(acc[i], 32);
@@ -620,13 +625,17 @@ __global__ __launch_bounds__(64) void k_down_quad(const uint4 *__restrict__ nib,
     const size_t tb = ((size_t)e * Td + 2 * blockIdx.x) * S;  // the two row tiles' first entry group
     const int place = lane & 31;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    quad_row_sums<QD>(
-        nib + tb * 64, scl + tb * 64, 2u * (uint32_t)S * 64u, (uint32_t)((lane >> 5) * S * 64 + place),
-        [&](int b) {
-            const int half = b >= S ? 1 : 0;
-            return (b - half * S) * 64 + 32 * half;
-        },
-        [&]() { stage_quad_rows(hq8, hsc, k0 + (lane < cnt ? lane : 0), ff, lds); }, lds, ff, acc);
+    auto rows = [&](auto np) {
+        quad_row_sums<QD, decltype(np)::value>(
+            nib + tb * 64, scl + tb * 64, 2u * (uint32_t)S * 64u, (uint32_t)((lane >> 5) * S * 64 + place),
+            [&](int b) {
+                const int half = b >= S ? 1 : 0;
+                return (b - half * S) * 64 + 32 * half;
+            },
+            [&]() { stage_quad_rows(hq8, hsc, k0 + (lane < cnt ? lane : 0), ff, lds); }, lds, ff, acc);
+    };
+    if (cnt <= 2) rows(std::integral_constant<int, 2>{});
+    else rows(std::integral_constant<int, 4>{});
     const int row = 64 * blockIdx.x + lane;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
