@@ -51,9 +51,16 @@ __device__ __forceinline__ double2 row_stats(const float4 (&wv)[F4], const float
         pf[4 * i + 2] = wv[i].z * xv[i].z;
         pf[4 * i + 3] = wv[i].w * xv[i].w;
     }
-    double c = 0.0;
+    // the lane's f64 sum as a pairwise tree (six dependent additions instead of C - 1 before the
+    // scan that the f32 prefixes below wait for)
+    double cd[C];
 #pragma unroll
-    for (int i = 0; i < C; ++i) c += (double)pf[i];
+    for (int i = 0; i < C; ++i) cd[i] = (double)pf[i];
+#pragma unroll
+    for (int st = 1; st < C; st *= 2)
+#pragma unroll
+        for (int i = 0; i + st < C; i += 2 * st) cd[i] += cd[i + st];
+    const double c = cd[0];
     const double incl = wave_scan_d(c);
     const double run = dpp_zero_d<0x138>(incl);  // wave_shr:1: the sum of the lanes below
     const double total = readlane_d(incl, 63);
