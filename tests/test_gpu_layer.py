@@ -104,7 +104,7 @@ def test_plan_matches_oracle(gpu, orc):
     rng = np.random.default_rng(6)
     # up to 8192 pairs a wave keeps its ids in registers between the count and the placement; above
     # that it reads them in batches (9001 and 40000: partial and several batches per wave)
-    for n_pairs in [8, 256, 3000, 4096, 8192, 9001, 40000]:
+    for n_pairs in [8, 256, 1000, 3000, 4096, 8192, 9001, 40000]:
         ids = (rng.zipf(1.2, n_pairs) % N_EXP).astype(np.int32)
         order, pos_of, gs = DevBuf(n_pairs * 4), DevBuf(n_pairs * 4), DevBuf((N_EXP + 1) * 4)
         hip.moe_plan(dev(ids), n_pairs, N_EXP, order, pos_of, gs)
@@ -123,6 +123,16 @@ def test_plan_matches_oracle(gpu, orc):
             assert np.array_equal(order.download(np.int32, o.size), o.astype(np.int32))
             assert np.array_equal(pos_of.download(np.int32, n_pairs), p.astype(np.int32))
             assert np.array_equal(gs.download(np.int32, N_EXP + 1), g.astype(np.int32))
+    # 256 experts (one thread of the plan's workgroup per expert, the group starts' last entry
+    # included)
+    for n_pairs in [700, 1024, 1025]:
+        ids = (rng.zipf(1.1, n_pairs) % 256).astype(np.int32)
+        order, pos_of, gs = DevBuf(n_pairs * 4), DevBuf(n_pairs * 4), DevBuf(257 * 4)
+        hip.moe_plan(dev(ids), n_pairs, 256, order, pos_of, gs)
+        o, p, g = orc.moe_plan(ids.astype(np.uint32), 256)
+        assert np.array_equal(order.download(np.int32, n_pairs), o.astype(np.int32)), n_pairs
+        assert np.array_equal(pos_of.download(np.int32, n_pairs), p.astype(np.int32)), n_pairs
+        assert np.array_equal(gs.download(np.int32, 257), g.astype(np.int32)), n_pairs
     # ids outside [0, n_exp) are left out of the plan
     ids = np.array([3, -1, 3, 200, 0], np.int32)
     order, pos_of, gs = DevBuf(20), DevBuf(20), DevBuf((N_EXP + 1) * 4)
